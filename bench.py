@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Decode-step attention benchmark on one MI355X (BASELINE.json metric).
+
+Workload (default ``--config cfg2``): Voxtral-Mini-3B decode shape, 30 layers,
+32 query / 8 KV heads, head_dim 128, bf16, batch 8, 7,500 audio + 64 text
+tokens per sequence; per layer 2 of 8 KV heads are class A (full KV), the
+others class B (512 rows).  Synthetic data: K, V ~ N(0, 1) times a
+per-(layer, KV head) scale from U(0.5, 2), q ~ N(0, 1).
+
+One step = for each of the 30 layers: in-place append of the step's K/V row
+to every segment (slack layout) + split-K decode attention.  All 30 layers
+have distinct buffers (~2.2 GB), far beyond the 256 MB Infinity Cache.  Each
+step is captured once as a HIP graph (two graphs: even/odd step, for the
+ping-ponged offsets) so the timed region measures the GPU, not Python.
+
+Reported:
+* value          -- whole-step throughput: algorithmic bytes (attention K/V
+                    rows + q/o + appended rows) of the K timed steps / wall time.
+* us_per_layer_step -- decode-attention kernel time per layer-step, from HIP
+                    events around back-to-back attention-only graph replays.
+* roofline       -- the attention kernel: algorithmic bytes per launch /
+                    average launch time vs 8 TB/s.
+* cpu_baseline   -- the float64 C oracle (1 core) on a bounded sample of the
+                    same layers.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode-attn µs/layer-step + achieved HBM TB/s (% of MI355X peak), 1 GPU"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg5"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "valu"])
+    ap.add_argument("--attn-reps", type=int, default=20, help="attention-only graph replays for the roofline")
+    ap.add_argument("--cpu-sample-layers", type=int, default=0,
+                    help="layers timed for the CPU baseline (0 = choose ~15 s of work)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    return ap.parse_args()
+
+
+class LayerState:
+    """Slack layout of one layer: each segment owns len + slack rows."""
+
+    def __init__(self, cfg, layer: int, slack: int, device, gen):
+        import numpy as np
+        import torch
+
+        self.n = cfg.n_seg
+        d = cfg.head_dim
+        lens = cfg.lengths[layer].astype(np.int64)
+        cap = lens + slack
+        cap = (cap + 7) // 8 * 8
+        base = np.zeros(self.n, np.int64)
+        base[1:] = np.cumsum(cap)[:-1]
+        self.pool_rows = int(cap.sum())
+        self.lens0 = lens
+        self.base = torch.from_numpy(base).to(device)
+        self.cap = torch.from_numpy(cap.astype(np.int32)).to(device)
+        cu = np.zeros(self.n + 1, np.int32)
+        cu[1:] = np.cumsum(lens)
+        self.cu = [torch.from_numpy(cu).to(device), torch.zeros(self.n + 1, dtype=torch.int32, device=device)]
+        self.cu_init = torch.from_numpy(cu).to(device)
+        scale_seg = np.tile(cfg.kv_scale[layer], cfg.batch).astype(np.float32)  # segment s = b * Hkv + h
+        row_scale = torch.from_numpy(np.repeat(scale_seg, cap)).to(device).unsqueeze(1)
+        self.k = (torch.randn(self.pool_rows, d, device=device, generator=gen) * row_scale).to(torch.bfloat16)
+        self.v = (torch.randn(self.pool_rows, d, device=device, generator=gen) * row_scale).to(torch.bfloat16)
+        self.q = torch.randn(self.n, cfg.group, d, device=device, generator=gen).to(torch.bfloat16)
+        self.new_k = torch.randn(self.n, d, device=device, generator=gen).to(torch.bfloat16)
+        self.new_v = torch.randn(self.n, d, device=device, generator=gen).to(torch.bfloat16)
+        self.out = torch.empty(self.n, cfg.group, d, dtype=torch.bfloat16, device=device)
+
+    def reset(self):
+        self.cu[0].copy_(self.cu_init)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path is single-GPU "
+              "per process and multi-GPU runs are not part of this build", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from wnw_amd import _lib, workloads
+    from wnw_amd.kv import fused_attn
+    from wnw_amd.kv.kernels import append_inplace
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.lib()
+    _lib.ensure_init(dev)
+    cfg = workloads.CONFIGS[args.config]()
+    L, N, G, D = cfg.layers, cfg.n_seg, cfg.group, cfg.head_dim
+    total_steps = args.warmup + args.steps
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    print(f"# config {cfg.name}: layers={L} n_seg={N} G={G} D={D} steps={args.steps} warmup={args.warmup}",
+          flush=True)
+    layers = [LayerState(cfg, l, total_steps + 2, dev, gen) for l in range(L)]
+    torch.cuda.synchronize()
+    ws = fused_attn.AttnWorkspace(dev)
+    ws.get(N, G, D)
+    scale = D ** -0.5
+
+    def step_launches(parity: int):
+        for st in layers:
+            cu_old, cu_new = st.cu[parity], st.cu[1 - parity]
+            append_inplace(st.k, st.v, st.new_k, st.new_v, cu_old, cu_new, st.base, st.cap)
+            fused_attn.decode_attn(st.q, st.k, st.v, cu_new, scale, seg_base=st.base, total_rows=st.pool_rows,
+                                   out=st.out, workspace=ws, kernel=args.kernel)
+
+    def attn_launches():
+        for st in layers:
+            fused_attn.decode_attn(st.q, st.k, st.v, st.cu[0], scale, seg_base=st.base, total_rows=st.pool_rows,
+                                   out=st.out, workspace=ws, kernel=args.kernel)
+
+    stream = torch.cuda.Stream(device=dev)
+    graphs = None
+    attn_graph = None
+    if not args.no_graph:
+        # capture on a side stream (default priority), then replay
+        with torch.cuda.stream(stream):
+            ws.get(N, G, D)
+        torch.cuda.synchronize()
+        graphs = []
+        for parity in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step_launches(parity)
+            graphs.append(g)
+        attn_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(attn_graph, stream=stream):
+            attn_launches()
+        torch.cuda.synchronize()
+        for st in layers:  # capture does not execute; start from the initial offsets
+            st.reset()
+        torch.cuda.synchronize()
+
+    def run_step(t: int):
+        if graphs is not None:
+            graphs[t % 2].replay()
+        else:
+            step_launches(t % 2)
+
+    # ---- warmup + timed decode steps --------------------------------------
+    ctx = torch.cuda.stream(stream) if graphs is not None else torch.cuda.stream(torch.cuda.current_stream())
+    with ctx:
+        for t in range(args.warmup):
+            run_step(t)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(args.warmup, total_steps):
+            run_step(t)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    assert _lib.device_error() == 0, "device error during the timed steps"
+    step_s = (t1 - t0) / args.steps
+
+    # bytes of the timed steps: rows attended at step t are lens0 + t + 1 per segment
+    attn_bytes_total = 0
+    append_bytes_total = 0
+    for t in range(args.warmup, total_steps):
+        for st in layers:
+            rows = int(st.lens0.sum()) + N * (t + 1)
+            attn_bytes_total += rows * D * 2 * 2 + 2 * N * G * D * 2
+            append_bytes_total += 2 * N * D * 2 * 2  # read new row + write it, K and V
+    value_tbs = (attn_bytes_total + append_bytes_total) / (t1 - t0) / 1e12
+
+    # ---- attention-only kernel timing (state after the timed steps) -------
+    # cu[0] now holds the offsets after an even number of steps, or cu[1]:
+    final_parity = total_steps % 2
+    for st in layers:
+        if final_parity == 1:
+            st.cu[0].copy_(st.cu[1])
+    torch.cuda.synchronize()
+    rows_attn = [int(st.cu[0][-1].item()) for st in layers]
+    bytes_per_launch = [r * D * 2 * 2 + 2 * N * G * D * 2 for r in rows_attn]
+    with torch.cuda.stream(stream):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        if attn_graph is not None:
+            attn_graph.replay()
+        else:
+            attn_launches()
+        ev0.record(stream)
+        for _ in range(args.attn_reps):
+            if attn_graph is not None:
+                attn_graph.replay()
+            else:
+                attn_launches()
+        ev1.record(stream)
+        ev1.synchronize()
+    attn_ms = ev0.elapsed_time(ev1)
+    launches = args.attn_reps * L
+    us_per_launch = attn_ms * 1e3 / launches
+    avg_bytes = float(np.mean(bytes_per_launch))
+    achieved_gbs = avg_bytes / (us_per_launch * 1e-6) / 1e9
+    assert _lib.device_error() == 0, "device error during attention timing"
+
+    # ---- CPU baseline: float64 C oracle on a bounded sample ---------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, layers, rows_attn, scale, args.cpu_sample_layers)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value_tbs, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": cfg.name, "layers": L, "batch": cfg.batch, "hq": cfg.hq, "hkv": cfg.hkv,
+                   "head_dim": D, "n_seg": N, "rows_per_layer_step": int(np.mean(rows_attn)),
+                   "kernel": args.kernel, "graph": graphs is not None, "notes": cfg.notes},
+        "us_per_layer_step": round(us_per_launch, 3),
+        "attn_TBs": round(achieved_gbs / 1e3, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", f"decode_attn_{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(cfg, layers, rows_attn, scale, sample_layers: int):
+    """Float64 C oracle (single core) on a bounded sample of the workload."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    D, G = cfg.head_dim, cfg.group
+    elapsed, done, bytes_done = 0.0, 0, 0
+    budget_s = 15.0
+    limit = sample_layers if sample_layers > 0 else len(layers)
+    for li, st in enumerate(layers[:limit]):
+        cu = st.cu[0].cpu().numpy()
+        base = st.base.cpu().numpy()
+        k = st.k.cpu().view(torch.int16).numpy().view(np.uint16)
+        v = st.v.cpu().view(torch.int16).numpy().view(np.uint16)
+        q = st.q.cpu().view(torch.int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=oracle.DT_BF16)
+        elapsed += time.perf_counter() - t0
+        done += 1
+        bytes_done += rows_attn[li] * D * 2 * 2 + 2 * cfg.n_seg * G * D * 2
+        if sample_layers <= 0 and elapsed > budget_s:
+            break
+    us = elapsed / done * 1e6
+    return {"value": round(bytes_done / elapsed / 1e9, 4), "unit": "GB/s", "us_per_layer_step": round(us, 1),
+            "cores": 1, "kind": "port",
+            "sample": f"{done} of {cfg.layers} layers of one decode step ({cfg.name}), float64 C oracle"}
+
+
+if __name__ == "__main__":
+    main()

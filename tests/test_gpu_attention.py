@@ -1,0 +1,192 @@
+"""GPU parity of the split-K decode attention against the float64 oracle.
+
+Tolerance: max-abs 2e-3 / max-rel 1e-2, applied as
+|got - ref| <= 2e-3 + 1e-2 * |ref| elementwise (bf16/f16 in, fp32 softmax
+and accumulation, output in the input dtype).  fp32 inputs are held to
+1e-4 / 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import DTYPE_CODES, allclose_report, cu_from_lens, from_torch, rand_rows, to_torch
+from wnw_amd import _lib
+from wnw_amd import workloads
+from wnw_amd.kv import fused_attn
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _tol(dtype):
+    return (1e-4, 1e-3) if dtype == "float32" else (ATOL, RTOL)
+
+
+def _run_case(dev, lens, G, D, dtype, kernel="auto", n_wg=0, scale=None, seed=0, kv_scale=1.0, base=None,
+              pool_rows=None):
+    rng = np.random.default_rng(seed)
+    n = len(lens)
+    cu = cu_from_lens(lens)
+    T = int(cu[-1])
+    scale = D ** -0.5 if scale is None else scale
+    q = rand_rows(rng, n * G, D, dtype).reshape(n, G, D)
+    rows = T if pool_rows is None else pool_rows
+    k = rand_rows(rng, rows, D, dtype, kv_scale)
+    v = rand_rows(rng, rows, D, dtype, kv_scale)
+    code = DTYPE_CODES[dtype]
+    ref = oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=code)
+    tq = to_torch(q, dtype, dev)
+    tk = to_torch(k, dtype, dev)
+    tv = to_torch(v, dtype, dev)
+    tcu = torch.from_numpy(cu).to(dev)
+    tb = None if base is None else torch.from_numpy(np.asarray(base, np.int64)).to(dev)
+    print(f"case n_seg={n} T={T} G={G} D={D} {dtype} kernel={kernel} n_wg={n_wg} seed={seed}", flush=True)
+    out = fused_attn.decode_attn(tq, tk, tv, tcu, scale, seg_base=tb, total_rows=T, kernel=kernel, n_wg=n_wg)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    got = oracle.to_f64(from_torch(out, dtype), code)
+    return got, ref
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("G", [1, 4, 7, 16])
+def test_small_ragged(gpu, kernel, dtype, G):
+    lens = [1, 2, 31, 32, 33, 64, 100, 257, 0, 5, 1000, 3]
+    got, ref = _run_case(gpu, lens, G, 128, dtype, kernel=kernel, seed=G)
+    ok, msg = allclose_report(got, ref, *_tol(dtype))
+    assert ok, msg
+    assert np.all(got[8] == 0)  # empty segment
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_head_dims(gpu, D):
+    got, ref = _run_case(gpu, [70, 1, 300, 129], 4, D, "bfloat16", seed=11)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_valu_head_dim_256(gpu):
+    got, ref = _run_case(gpu, [70, 1, 300, 129], 4, 256, "bfloat16", kernel="valu", seed=12)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("n_wg", [1, 2, 3, 7, 64, 333, 2048])
+def test_split_counts_agree(gpu, n_wg):
+    """Any stream-K split must give the no-split result (log-sum-exp merge identity)."""
+    lens = [513, 7565, 1, 90, 2048, 4]
+    got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", n_wg=n_wg, seed=5)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_more_workgroups_than_rows(gpu):
+    got, ref = _run_case(gpu, [1, 0, 2, 1], 4, 128, "bfloat16", n_wg=50, seed=6)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_all_segments_empty(gpu):
+    got, ref = _run_case(gpu, [0, 0, 0], 4, 128, "bfloat16", seed=7)
+    assert np.all(got == 0)
+
+
+def test_single_row_returns_v_exactly(gpu):
+    """One key: softmax weight is exactly 1, so the output equals the V row bit for bit."""
+    rng = np.random.default_rng(8)
+    n, G, D = 40, 4, 128
+    q = rand_rows(rng, n * G, D, "bfloat16").reshape(n, G, D)
+    k = rand_rows(rng, n, D, "bfloat16")
+    v = rand_rows(rng, n, D, "bfloat16")
+    cu = np.arange(n + 1, dtype=np.int32)
+    out = fused_attn.decode_attn(to_torch(q, "bfloat16", gpu), to_torch(k, "bfloat16", gpu),
+                                 to_torch(v, "bfloat16", gpu), torch.from_numpy(cu).to(gpu), 0.088)
+    got = from_torch(out, "bfloat16")
+    for g in range(G):
+        np.testing.assert_array_equal(got[:, g, :], v)
+
+
+def test_slack_layout_with_seg_base(gpu):
+    lens = [40, 0, 700, 33, 1]
+    caps = [64, 8, 800, 40, 9]
+    base = np.zeros(5, np.int64)
+    pos = 3
+    for s in (4, 2, 0, 3, 1):  # physical order differs from logical
+        base[s] = pos
+        pos += caps[s] + 5
+    got, ref = _run_case(gpu, lens, 7, 128, "bfloat16", seed=9, base=base, pool_rows=pos + 10)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_repeated_launches_reuse_workspace(gpu):
+    """Counters are left at zero: many launches with different shapes stay correct."""
+    for i, lens in enumerate([[300, 5000, 12], [7, 7, 7, 7, 7000], [1, 2, 3], [6000, 6000]]):
+        got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", seed=20 + i)
+        ok, msg = allclose_report(got, ref, ATOL, RTOL)
+        assert ok, msg
+
+
+def test_cfg1_fp32_and_bf16(gpu):
+    """Config 1 (fp32 plumbing) through the VALU kernel, and its bf16 cast through MFMA."""
+    cfg = workloads.config1()
+    lens = cfg.lengths[0] + 1
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "float32", seed=0)
+    ok, msg = allclose_report(got, ref, 1e-4, 1e-3)
+    assert ok, msg
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=0)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("name,layer", [("cfg2", 0), ("cfg3", 0), ("cfg5", 0)])
+def test_config_layer_full_size(gpu, name, layer):
+    """One full-size layer of configs 2, 3 and 5 against the float64 oracle."""
+    cfg = workloads.CONFIGS[name]()
+    lens = cfg.lengths[layer] + 1
+    kvs = float(cfg.kv_scale[layer].mean())
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=layer, kv_scale=kvs)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    print(name, msg)
+    assert ok, msg
+
+
+def test_large_scores_are_stable(gpu):
+    """Keys scaled x8: scores up to ~+-100 must not overflow the online softmax."""
+    got, ref = _run_case(gpu, [2000, 33, 517], 4, 128, "bfloat16", seed=30, kv_scale=8.0)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_q1_decode_attn_reference_signature(gpu):
+    rng = np.random.default_rng(31)
+    lens = [100, 3000, 7]
+    cu = cu_from_lens(lens)
+    q = rand_rows(rng, 3 * 4, 128, "bfloat16").reshape(3, 4, 128)
+    k = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
+    v = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
+    ref = oracle.decode_attn(q, k, v, cu, 0.1, dtype=oracle.DT_BF16)
+    out = fused_attn.q1_decode_attn(to_torch(q, "bfloat16", gpu), to_torch(k, "bfloat16", gpu),
+                                    to_torch(v, "bfloat16", gpu), torch.from_numpy(cu).to(gpu), 0.1)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (3, 4, 128)
+    ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_bad_offsets_are_refused_not_read(gpu):
+    """A segment pointing past the K/V rows sets the device error word instead of faulting."""
+    n, G, D = 2, 4, 128
+    q = torch.zeros(n, G, D, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(64, D, dtype=torch.bfloat16, device=gpu)
+    cu = torch.tensor([0, 10, 20], dtype=torch.int32, device=gpu)
+    base = torch.tensor([0, 60], dtype=torch.int64, device=gpu)  # 60 + 10 > 64
+    fused_attn.decode_attn(q, k, k, cu, 0.1, seg_base=base, total_rows=20)
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_BOUNDS
+    # the workspace is still usable afterwards
+    got, ref = _run_case(gpu, [50, 60], 4, 128, "bfloat16", seed=40)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg

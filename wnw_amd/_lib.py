@@ -1,0 +1,117 @@
+"""Loader of ``libwnw_amd.so``, the C ABI of the gfx950 kernels.
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``make -C wnw_amd/csrc``).  Everything here fails loudly: there is no CPU or
+PyTorch fallback for any operator of this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # loads torch's HIP runtime first; the library binds to it
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwnw_amd.so")
+
+WNW_OK, WNW_EINVAL, WNW_EHIP, WNW_ENOTSUP = 0, 1, 2, 3
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
+ATTN_AUTO, ATTN_MFMA, ATTN_VALU = 0, 1, 2
+DEVERR_BOUNDS, DEVERR_ORDER, DEVERR_CAPACITY = 1, 2, 4
+
+_TORCH_DTYPES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
+
+_lib: ctypes.CDLL | None = None
+
+_vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/wnw_amd.h
+_SIGNATURES = {
+    "wnw_last_error": (ctypes.c_char_p, []),
+    "wnw_abi_version": (_i32, []),
+    "wnw_init": (_i32, []),
+    "wnw_device_error": (_i32, [_i32]),
+    "wnw_interleave_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
+    "wnw_append_inplace": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
+    "wnw_rebuild_append_kv": (_i32, [_vp] * 13 + [_i64] * 7 + [_i32, _vp, _vp, _vp]),
+    "wnw_compact_segments": (_i32, [_vp] * 9 + [_i64, _i64, _i64] + [_vp] * 9 + [_i64, _i32, _i64, _i64, _i64,
+                                                                           _i64, _i32, _vp]),
+    "wnw_decode_attn_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "wnw_workspace_init": (_i32, [_vp, _i64, _vp]),
+    "wnw_decode_attn": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp, _vp,
+                               _i64, _vp]),
+    "wnw_decode_attn_ex": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp, _vp,
+                                  _i64, _i32, _i64, _vp]),
+}
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the HIP extension first "
+                "(python -c 'import __graft_entry__ as g; g.build()')")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+class WnwError(RuntimeError):
+    pass
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != WNW_OK:
+        msg = lib().wnw_last_error().decode(errors="replace")
+        raise WnwError(f"{what}: status {rc}: {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _TORCH_DTYPES[dt]
+    except KeyError:
+        raise WnwError(f"unsupported dtype {dt}") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    """Raise unless every tensor lives on a HIP device (no CPU fallback)."""
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise WnwError(f"wnw_amd kernels need GPU tensors, got a tensor on {t.device}")
+
+
+def device_error(clear: bool = True) -> int:
+    """WNW_DEVERR_* bits recorded by kernels on the current device (syncs)."""
+    v = lib().wnw_device_error(1 if clear else 0)
+    if v < 0:
+        raise WnwError("wnw_device_error failed")
+    return v
+
+
+_init_done: set[int] = set()
+
+
+def ensure_init(device: torch.device) -> None:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _init_done:
+        return
+    with torch.cuda.device(idx):
+        check(lib().wnw_init(), "wnw_init")
+    _init_done.add(idx)

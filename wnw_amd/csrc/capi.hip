@@ -1,0 +1,72 @@
+// Library-wide host glue of the C ABI: thread-local error messages, the
+// per-device error word that kernels set instead of reading out of bounds,
+// and version queries.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <mutex>
+#include <vector>
+
+#include "wnw_common.h"
+
+namespace wnw {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  set_error("%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+  return WNW_EHIP;
+}
+
+static std::mutex g_mu;
+static std::vector<int32_t*> g_err_words;
+
+// Allocates (once per device, zero-filled synchronously) the word kernels
+// record WNW_DEVERR_* bits into.  Returns null if the allocation failed, in
+// which case kernels skip the recording but still refuse bad offsets.
+int32_t* device_error_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_mu);
+  if ((int)g_err_words.size() <= dev) g_err_words.resize(dev + 1, nullptr);
+  if (!g_err_words[dev]) {
+    void* p = nullptr;
+    if (hipMalloc(&p, 256) != hipSuccess) return nullptr;
+    if (hipMemset(p, 0, 256) != hipSuccess) return nullptr;
+    g_err_words[dev] = (int32_t*)p;
+  }
+  return g_err_words[dev];
+}
+
+}  // namespace wnw
+
+extern "C" const char* wnw_last_error(void) { return wnw::g_err; }
+
+extern "C" int wnw_abi_version(void) { return 1; }
+
+extern "C" int wnw_init(void) {
+  if (!wnw::device_error_word()) {
+    wnw::set_error("could not allocate the device error word");
+    return WNW_EHIP;
+  }
+  return WNW_OK;
+}
+
+extern "C" int wnw_device_error(int clear) {
+  int32_t* w = wnw::device_error_word();
+  if (!w) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  int32_t v = 0;
+  if (hipMemcpy(&v, w, 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  if (clear && v != 0) {
+    if (hipMemset(w, 0, 4) != hipSuccess) return -1;
+  }
+  return v;
+}

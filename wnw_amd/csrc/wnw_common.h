@@ -1,0 +1,130 @@
+// Shared host/device helpers of the gfx950 kernels: element types, bf16/f16
+// conversions, wave-level exchanges, error reporting.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wnw_amd.h"
+
+namespace wnw {
+
+// ---------------------------------------------------------------------------
+// host-side error reporting
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+// Per-device error word (allocated once per device by the library).
+int32_t* device_error_word();
+
+#define WNW_CHECK_ARG(cond, ...)       \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::wnw::set_error(__VA_ARGS__);   \
+      return WNW_EINVAL;               \
+    }                                  \
+  } while (0)
+
+#define WNW_CHECK_HIP(expr, what)                         \
+  do {                                                    \
+    hipError_t e_ = (expr);                               \
+    if (e_ != hipSuccess) return ::wnw::hip_fail(e_, what); \
+  } while (0)
+
+inline int elem_bytes(int dtype) { return dtype == WNW_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// element types
+// ---------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element traits: load one element as float / store float as element.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static float to_f32(const float* p, int64_t i) { return p[i]; }
+  __device__ static void store(float* p, int64_t i, float x) { p[i] = x; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static float to_f32(const bf16_t* p, int64_t i) {
+    return __uint_as_float(((uint32_t)p[i].bits) << 16);
+  }
+  __device__ static void store(bf16_t* p, int64_t i, float x) {
+    p[i].bits = (uint16_t)f32_to_bf16_bits(x);
+  }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static float to_f32(const f16_t* p, int64_t i) { return f16_bits_to_f32(p[i].bits); }
+  __device__ static void store(f16_t* p, int64_t i, float x) {
+    p[i].bits = (uint16_t)f32_to_f16_bits(x);
+  }
+};
+
+// Unpack 8 packed 16-bit elements (one 16-byte chunk) to fp32.
+__device__ __forceinline__ void unpack8(const u32x4& w, float* f, bf16_t*) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(w[i]);
+    f[2 * i + 1] = bf16_hi(w[i]);
+  }
+}
+__device__ __forceinline__ void unpack8(const u32x4& w, float* f, f16_t*) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+    f[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wave-level exchanges (wave64)
+// ---------------------------------------------------------------------------
+// x from lane (lane ^ 16), within each 32-lane half.
+__device__ __forceinline__ float swap16(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
+// x from lane (lane ^ 32).
+__device__ __forceinline__ float swap32(float x) { return __shfl_xor(x, 32); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ void raise_device_error(int32_t* err, int bits) {
+  if (err) atomicOr(err, bits);
+}
+
+}  // namespace wnw

@@ -1,0 +1,129 @@
+"""q = 1 GQA decode attention over the flat varlen KV layout.
+
+Mirrors ``src/common/kv/fused_attn.py`` of the reference (``q1_decode_attn``)
+and stands in for its default ``varlen_attn`` call
+(src/algorithms/wnw/code/session.py:90-106).  The computation is the gfx950
+split-K kernel ``wnw_decode_attn`` of ``libwnw_amd.so``: the rows of all
+segments are divided evenly over the workgroups, partial softmax states are
+merged by the last workgroup to finish a segment, so ragged segment lengths
+never leave CUs idle (the reference runs one program per segment).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+
+class AttnWorkspace:
+    """Split-K workspace of one (device, stream): partials + arrival counters.
+
+    The kernel leaves the counters at zero after every launch, so a
+    workspace is cleared once at allocation and then reused; two streams
+    must not share one (launches on one stream are ordered).
+    """
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.buf: torch.Tensor | None = None
+        self.counter_cap = 0  # n_seg whose counter region is known to be zero
+
+    def get(self, n_seg: int, group: int, head_dim: int) -> tuple[torch.Tensor, int]:
+        need = int(_lib.lib().wnw_decode_attn_workspace_bytes(n_seg, group, head_dim))
+        if need < 0:
+            raise _lib.WnwError("bad workspace query")
+        if self.buf is None or self.buf.numel() < need:
+            size = max(need, 1 << 20)
+            self.buf = torch.empty(size, dtype=torch.uint8, device=self.device)
+            self.counter_cap = 0
+        if n_seg > self.counter_cap:
+            # counters sit at the front, sized by n_seg: a larger n_seg reaches
+            # into bytes that held partials, so the buffer is cleared again.
+            _lib.check(_lib.lib().wnw_workspace_init(_lib.ptr(self.buf), self.buf.numel(),
+                                                     _lib.stream_of(self.device)), "workspace init")
+            self.counter_cap = n_seg
+        return self.buf, self.buf.numel()
+
+
+_workspaces: dict[tuple[int, int], AttnWorkspace] = {}
+
+
+def workspace_for(device: torch.device) -> AttnWorkspace:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None:
+        ws = AttnWorkspace(torch.device("cuda", idx))
+        _workspaces[key] = ws
+    return ws
+
+
+_KERNELS = {"auto": _lib.ATTN_AUTO, "mfma": _lib.ATTN_MFMA, "valu": _lib.ATTN_VALU}
+
+
+def decode_attn(
+    q_flat: torch.Tensor,
+    k_flat: torch.Tensor,
+    v_flat: torch.Tensor,
+    cu_k: torch.Tensor,
+    scale: float,
+    *,
+    seg_base: torch.Tensor | None = None,
+    total_rows: int | None = None,
+    out: torch.Tensor | None = None,
+    workspace: AttnWorkspace | None = None,
+    kernel: str = "auto",
+    n_wg: int = 0,
+) -> torch.Tensor:
+    """Decode attention with the layout extensions of this package.
+
+    ``seg_base`` (int64 [N]) gives each segment's physical first row in
+    ``k_flat``/``v_flat`` (slack layout); ``total_rows`` is an upper bound of
+    ``cu_k[-1]`` (defaults to ``k_flat.shape[0]``, exact for the dense layout).
+    """
+    _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, seg_base)
+    if q_flat.dim() != 3:
+        raise _lib.WnwError(f"q_flat must be [N, G, D], got {tuple(q_flat.shape)}")
+    nseg, g, d = q_flat.shape
+    if k_flat.dim() != 2 or k_flat.shape[1] != d or v_flat.shape != k_flat.shape:
+        raise _lib.WnwError(f"k/v must be [rows, {d}] and equal: {tuple(k_flat.shape)} {tuple(v_flat.shape)}")
+    if q_flat.dtype != k_flat.dtype or v_flat.dtype != k_flat.dtype:
+        raise _lib.WnwError("q, k and v must share a dtype")
+    if cu_k.dtype != torch.int32 or cu_k.numel() != nseg + 1:
+        raise _lib.WnwError("cu_k must be int32 [N+1]")
+    if seg_base is not None and (seg_base.dtype != torch.int64 or seg_base.numel() != nseg):
+        raise _lib.WnwError("seg_base must be int64 [N]")
+    if k_flat.shape[0] > 0 and (k_flat.stride(1) != 1 or k_flat.stride(0) != d or v_flat.stride(1) != 1
+                                or v_flat.stride(0) != d):
+        raise _lib.WnwError("k_flat / v_flat rows must be contiguous [rows, D]")
+    q_flat = q_flat.contiguous()
+    cu_k = cu_k.contiguous()
+    if out is None:
+        out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
+    rows = k_flat.shape[0] if total_rows is None else int(total_rows)
+    _lib.ensure_init(q_flat.device)
+    ws = workspace if workspace is not None else workspace_for(q_flat.device)
+    buf, nbytes = ws.get(nseg, g, d)
+    _lib.check(_lib.lib().wnw_decode_attn_ex(
+        _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base),
+        nseg, g, d, rows, k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out),
+        _lib.ptr(buf), nbytes, _KERNELS[kernel], int(n_wg), _lib.stream_of(q_flat.device)), "decode_attn")
+    return out
+
+
+def q1_decode_attn(
+    q_flat: torch.Tensor,
+    k_flat: torch.Tensor,
+    v_flat: torch.Tensor,
+    cu_k: torch.Tensor,
+    scale: float,
+    block_n: int = 64,
+) -> torch.Tensor:
+    """Return attention output [nseg, G, D] (same dtype as q_flat).
+
+    Reference: ``q1_decode_attn`` (src/common/kv/fused_attn.py:47-65).
+    ``block_n`` is accepted for signature compatibility; the tile shape of
+    the gfx950 kernel is fixed (32-row MFMA steps).
+    """
+    del block_n
+    return decode_attn(q_flat, k_flat, v_flat, cu_k, scale)
