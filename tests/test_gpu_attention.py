@@ -110,16 +110,45 @@ def test_single_row_returns_v_exactly(gpu):
 
 
 def test_slack_layout_with_seg_base(gpu):
-    lens = [40, 0, 700, 33, 1]
-    caps = [64, 8, 800, 40, 9]
-    base = np.zeros(5, np.int64)
+    """Per-segment slack: segments in index order with gaps (garbage rows between)."""
+    lens = [40, 0, 700, 33, 1, 129]
+    caps = [64, 8, 800, 40, 9, 200]
+    base = np.zeros(len(lens), np.int64)
     pos = 3
-    for s in (4, 2, 0, 3, 1):  # physical order differs from logical
+    for s in range(len(lens)):
         base[s] = pos
         pos += caps[s] + 5
     got, ref = _run_case(gpu, lens, 7, 128, "bfloat16", seed=9, base=base, pool_rows=pos + 10)
     ok, msg = allclose_report(got, ref, ATOL, RTOL)
     assert ok, msg
+
+
+def test_slack_layout_many_workgroups(gpu):
+    """Slack layout where workgroup ranges start inside gaps (speculative loads discarded)."""
+    rng = np.random.default_rng(19)
+    lens = rng.integers(1, 400, size=40)
+    base = np.zeros(40, np.int64)
+    pos = 0
+    for s in range(40):
+        pos += int(rng.integers(0, 70))  # gap
+        base[s] = pos
+        pos += int(lens[s])
+    for n_wg in (0, 17, 333):
+        got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", seed=19, base=base, pool_rows=pos + 3, n_wg=n_wg)
+        ok, msg = allclose_report(got, ref, ATOL, RTOL)
+        assert ok, msg
+
+
+def test_out_of_order_layout_is_flagged(gpu):
+    """Segments must be laid out in index order; a violation sets the device error word."""
+    n, G, D = 3, 4, 128
+    q = torch.zeros(n, G, D, dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros(100, D, dtype=torch.bfloat16, device=gpu)
+    cu = torch.tensor([0, 10, 20, 30], dtype=torch.int32, device=gpu)
+    base = torch.tensor([50, 0, 70], dtype=torch.int64, device=gpu)  # segment 0 after segment 1
+    fused_attn.decode_attn(q, k, k, cu, 0.1, seg_base=base)
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_ORDER
 
 
 def test_repeated_launches_reuse_workspace(gpu):

@@ -6,16 +6,19 @@
 //     out[s, g] = sum_r softmax_r(scale * q[s, g] . K[r]) * V[r]
 // over the rows r of segment s.
 //
-// Work split ("stream-K" over the logical row space).  The T = cu[n_seg]
-// logical rows are cut into P equal contiguous ranges, one per workgroup, so
-// every workgroup streams the same number of K/V bytes however ragged the
-// segment lengths are.  A range may cover the tail of one segment, whole
-// segments and the head of another; each (workgroup, segment) overlap is a
-// "piece".  A piece that is a whole segment writes the output directly.  The
-// others write an (m, l, acc) partial to slot (p + s) -- unique because
-// ranges and segments are both monotone in the row space -- and bump the
-// segment's arrival counter; the last arriver merges the partials by
-// log-sum-exp and writes the output (no second kernel launch).
+// Work split ("stream-K" over the physical row space).  The kv_rows physical
+// rows of K/V are cut into P equal contiguous ranges, one per workgroup, so
+// every workgroup streams the same number of bytes however ragged the
+// segment lengths are.  Segments
+// must be laid out in index order (base[s] + len[s] <= base[s+1]; the dense
+// layout and a per-segment slack layout both are); the kernel checks it.
+// A range may cover the tail of one segment, whole segments and the head of
+// another; each (workgroup, segment) overlap is a "piece".  A piece that is a
+// whole segment writes the output directly.  The others write an (m, l, acc)
+// partial to slot (p + s) -- unique because ranges and segments are both
+// monotone in the row space -- and bump the segment's arrival counter; the
+// last arriver merges the partials by log-sum-exp and writes the output (no
+// second kernel launch).
 //
 // Inside a workgroup the NW waves take 32-row (MFMA) or 64-row (VALU) steps of
 // the piece round-robin, each keeping an online-softmax state; the wave states
@@ -56,96 +59,105 @@ struct AttnParams {
 
 // Per-workgroup schedule, shared through LDS.
 struct SchedLds {
-  int64_t T;
-  int64_t B0, B1;
-  int32_t P;  // effective number of workgroups (<= T)
+  int64_t R;       // rows partitioned (kv_rows)
+  int64_t B0, B1;  // this workgroup's physical row range
+  int32_t P;       // effective number of workgroups (<= R)
   int32_t s_first, s_last;
   int32_t is_last;  // combine flag broadcast
-  int32_t ring_lo[kRing];
-  int32_t ring_hi[kRing];
   int64_t ring_base[kRing];
+  int32_t ring_len[kRing];
 };
 
-__device__ __forceinline__ int64_t range_start(int64_t p, int64_t T, int64_t P) {
-  return (p * T) / P;
+__device__ __forceinline__ int64_t range_start(int64_t p, int64_t R, int64_t P) {
+  return (p * R) / P;
 }
-// The workgroup whose row range holds logical row j (P <= T).
-__device__ __forceinline__ int64_t owner_of(int64_t j, int64_t T, int64_t P) {
-  return ((j + 1) * P - 1) / T;
+// The workgroup whose row range holds physical row j (P <= R).
+__device__ __forceinline__ int64_t owner_of(int64_t j, int64_t R, int64_t P) {
+  return ((j + 1) * P - 1) / R;
+}
+__device__ __forceinline__ int64_t effective_wgs(int64_t R) {
+  return R > 0 ? min((int64_t)gridDim.x, R) : 0;
 }
 
-// Workgroup prologue: one pass over cu (all threads, independent loads) finds
-// T, this workgroup's row range, the overlapping segments, and writes zero
-// outputs for the empty segments this workgroup owns.
+// Workgroup prologue: one pass over cu / base (all threads, independent
+// loads) finds the segments whose rows overlap this workgroup's range,
+// checks the layout, and writes the outputs of empty segments (zeros) and of
+// invalid ones (NaN) owned by this workgroup (segment i -> workgroup i % grid).
 template <typename T, int NT>
-__device__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
+__device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
   const int tid = threadIdx.x;
   const int N = p.n_seg;
   if (tid == 0) {
     sl.s_first = 0x7fffffff;
     sl.s_last = -1;
   }
-  // All loads of the first chunk are issued before the barrier so the
-  // prologue costs one global round trip for n_seg <= 4 * NT.
-  const int64_t Ttot = p.cu[N];
-  int32_t lo[4], hi[4];
-  int64_t bs[4];
+  const int64_t R = p.kv_rows;
+  const int64_t P = effective_wgs(R);
+  const int64_t pid = blockIdx.x;
+  const bool active = pid < P;
+  const int64_t B0 = active ? range_start(pid, R, P) : 0;
+  const int64_t B1 = active ? range_start(pid + 1, R, P) : 0;
+  int32_t lo[4], hi[4], nxt[4];
+  int64_t bs[4], bn[4];
+  const WNW_GLOBAL int32_t* cu = gptr<int32_t>(p.cu);
+  const WNW_GLOBAL int64_t* basep = gptr<int64_t>(p.base);
   auto load_chunk = [&](int i0) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * NT + tid;
-      lo[u] = 0;
-      hi[u] = 0;
-      bs[u] = 0;
+      lo[u] = hi[u] = nxt[u] = 0;
+      bs[u] = bn[u] = 0;
       if (i < N) {
-        lo[u] = p.cu[i];
-        hi[u] = p.cu[i + 1];
-        if (p.base) bs[u] = p.base[i];
+        lo[u] = cu[i];
+        hi[u] = cu[i + 1];
+        if (p.base) {
+          bs[u] = basep[i];
+          if (i + 1 < N) bn[u] = basep[i + 1];
+        } else if (i + 1 < N) {
+          nxt[u] = 1;
+        }
       }
     }
   };
+  // The loads of the first chunk are issued before the barrier: one global
+  // round trip for n_seg <= 4 * NT.
   load_chunk(0);
   __syncthreads();
-  const int64_t P = Ttot > 0 ? min((int64_t)gridDim.x, Ttot) : 0;
-  const int64_t pid = blockIdx.x;
-  const bool active = pid < P;
-  const int64_t B0 = active ? range_start(pid, Ttot, P) : 0;
-  const int64_t B1 = active ? range_start(pid + 1, Ttot, P) : 0;
   for (int i0 = 0; i0 < N; i0 += 4 * NT) {
     if (i0 > 0) load_chunk(i0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * NT + tid;
       if (i >= N) continue;
-      if (hi[u] < lo[u]) {  // corrupt offsets: treated as an empty segment
+      int64_t len = (int64_t)hi[u] - lo[u];
+      const int64_t b = p.base ? bs[u] : (int64_t)lo[u];
+      if (len < 0) {  // corrupt offsets: treated as an empty segment
         raise_device_error(p.err, WNW_DEVERR_ORDER);
-        hi[u] = lo[u];
+        len = 0;
       }
-      if (hi[u] == lo[u]) {
-        bool own = false;
-        if (Ttot == 0) {
-          own = (pid == 0);
-        } else if (active) {
-          own = (lo[u] >= B0 && lo[u] < B1) || (lo[u] == Ttot && pid == P - 1);
-        }
-        if (own) {
+      // layout order: segment i must end before segment i + 1 starts
+      if (p.base && i + 1 < N && b + len > bn[u]) raise_device_error(p.err, WNW_DEVERR_ORDER);
+      (void)nxt;
+      const bool owner = (i % (int)gridDim.x) == (int)pid;
+      if (len == 0 || b < 0 || b + len > R) {
+        if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+        if (owner) {
           T* o = (T*)p.out + (int64_t)i * p.G * D;
-          for (int e = 0; e < p.G * D; ++e) Elem<T>::store(o, e, 0.f);
+          const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
+          for (int e = 0; e < p.G * D; ++e) Elem<T>::store(o, e, fill);
         }
+        continue;
       }
-      // Ring membership uses "touching" ranges so every segment between
-      // s_first and s_last (including empty ones) has a valid entry.
-      if (active && lo[u] <= B1 && hi[u] >= B0) {
+      if (active && b < B1 && b + len > B0) {
         atomicMin(&sl.s_first, i);
         atomicMax(&sl.s_last, i);
-        sl.ring_lo[i % kRing] = lo[u];
-        sl.ring_hi[i % kRing] = hi[u];
-        sl.ring_base[i % kRing] = p.base ? bs[u] : (int64_t)lo[u];
+        sl.ring_base[i % kRing] = b;
+        sl.ring_len[i % kRing] = (int32_t)len;
       }
     }
   }
   if (tid == 0) {
-    sl.T = Ttot;
+    sl.R = R;
     sl.P = (int32_t)P;
     sl.B0 = B0;
     sl.B1 = B1;
@@ -154,33 +166,47 @@ __device__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
 }
 
 struct Piece {
-  int64_t seg_lo, seg_hi;  // logical segment bounds
-  int64_t phys;            // physical row of the piece's first row
-  int32_t nrows;           // rows in the piece (-1 if the segment lies outside K/V)
+  int64_t seg_base;  // physical first row of the segment
+  int64_t seg_len;
+  int64_t phys;      // physical row of the piece's first row
+  int32_t nrows;     // rows in the piece
   bool whole;
-  bool skip;               // no rows of this segment in the workgroup's range
+  bool skip;         // no valid rows of this segment in the workgroup's range
 };
+
+// Workgroup-uniform values read from LDS land in VGPRs; broadcasting them
+// from lane 0 puts them in SGPRs, so addresses and loop bounds derived from
+// them stay scalar.
+__device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 __device__ __forceinline__ Piece make_piece(const AttnParams& p, const SchedLds& sl, int s) {
   Piece pc;
-  int64_t lo, hi, b;
+  int64_t b, len;
   if (sl.s_last - sl.s_first < kRing) {
-    lo = sl.ring_lo[s % kRing];
-    hi = sl.ring_hi[s % kRing];
     b = sl.ring_base[s % kRing];
+    len = sl.ring_len[s % kRing];
   } else {
-    lo = p.cu[s];
-    hi = p.cu[s + 1];
-    b = p.base ? p.base[s] : lo;
+    const int64_t lo = gptr<int32_t>(p.cu)[s], hi = gptr<int32_t>(p.cu)[s + 1];
+    b = p.base ? gptr<int64_t>(p.base)[s] : lo;
+    len = hi - lo;
   }
-  pc.seg_lo = lo;
-  pc.seg_hi = hi;
-  pc.skip = !(hi > lo && lo < sl.B1 && hi > sl.B0);
-  const int64_t a = max(lo, sl.B0), e = min(hi, sl.B1);
-  pc.whole = (a == lo) && (e == hi);
-  pc.phys = b + (a - lo);
-  pc.nrows = (int32_t)(e - a);
-  if (b < 0 || b + (hi - lo) > p.kv_rows) pc.nrows = -1;  // caller flags it
+  b = uni(b);
+  len = uni(len);
+  pc.seg_base = b;
+  pc.seg_len = len;
+  // Invalid or empty segments inside [s_first, s_last] are skipped here and
+  // handled by their owner in schedule(); the condition matches it exactly.
+  pc.skip = !(len > 0 && b >= 0 && b + len <= uni(sl.R) && b < uni(sl.B1) && b + len > uni(sl.B0));
+  const int64_t B0 = uni(sl.B0), B1 = uni(sl.B1);
+  const int64_t a = max(b, B0), e = min(b + len, B1);
+  pc.whole = (a == b) && (e == b + len);
+  pc.phys = a;
+  pc.nrows = pc.skip ? 0 : (int32_t)(e - a);
   return pc;
 }
 
@@ -196,6 +222,93 @@ __device__ __forceinline__ float ld_agent(const float* p) {
 }
 // s_waitcnt vmcnt(0): every vector memory access of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt not waited on), n < 64.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N & 0x30) << 10));
+}
+
+// Last-arriver merge of the np partials of one segment (slots s0 .. s0+np-1)
+// into the output.  The partials of consecutive slots are contiguous, so a
+// chunk of pieces is one contiguous block: it is copied straight into LDS
+// with agent-coherent (sc1) direct global->LDS loads, together with the
+// pieces' (m, l), at the cost of one memory round trip and almost no
+// registers.  Summation order is fixed, so results are deterministic.
+// `lds` / `lds_bytes` is the workgroup's LDS, free at this point.
+template <typename T, int NT>
+__device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, T* o,
+                                               uint8_t* lds, int lds_bytes) {
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int G = p.G;
+  const int GD = G * D;
+  float* gm = (float*)lds;                    // [3][16]: M, L, rescale
+  float* wm = gm + 3 * kMaxGroup;             // [pch][G] m, then weights
+  const int head = 3 * kMaxGroup * 4;         // bytes before the per-piece tables
+  // pieces per chunk: tables (8 * G bytes each) + accumulators (4 * GD bytes each)
+  const int room = (lds_bytes - head - 1024) / (4 * GD + 8 * G);
+  const int pch = max(1, min(np, room));
+  float* wl = wm + pch * G;                   // [pch][G] l
+  uint8_t* accl = (uint8_t*)(((uintptr_t)(wl + pch * G) + 1023) & ~(uintptr_t)1023);  // [pch][GD]
+  const int ept = (GD + NT - 1) / NT;
+  float accv[kMaxGroup * 256 / 256];          // up to 16 elements per thread (G * D <= 4096)
+#pragma unroll
+  for (int e = 0; e < kMaxGroup * 256 / 256; ++e) accv[e] = 0.f;
+  for (int q0 = 0; q0 < np; q0 += pch) {
+    const int nq = min(pch, np - q0);
+    // accumulators: nq * GD floats, contiguous, 1 KB per wave-wide load
+    const int nvec = nq * GD / 4;
+    const WNW_GLOBAL float* src = gptr<float>(p.part_acc + (s0 + q0) * GD);
+    for (int k = w; k * 64 < nvec; k += NT / 64) {
+      const int v = k * 64 + lane;
+      if (v < nvec) __builtin_amdgcn_global_load_lds(src + 4 * v, accl + k * 1024, 16, 0, 16);
+    }
+    for (int j = tid; j < nq * G; j += NT) {
+      const int64_t sq = s0 + q0 + j / G;
+      const int g = j % G;
+      wm[j] = ld_agent(p.part_ml + (sq * G + g) * 2);
+      wl[j] = ld_agent(p.part_ml + (sq * G + g) * 2 + 1);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (tid < G) {  // running max and sum per head, rescale of what is merged so far
+      const int g = tid;
+      const float M = q0 == 0 ? kNegBig : gm[g];
+      float L = q0 == 0 ? 0.f : gm[kMaxGroup + g];
+      float Mn = M;
+      for (int q = 0; q < nq; ++q) Mn = fmaxf(Mn, wm[q * G + g]);
+      const float so = exp2f(M - Mn);
+      L *= so;
+      for (int q = 0; q < nq; ++q) {
+        const float wq = exp2f(wm[q * G + g] - Mn);
+        L += wl[q * G + g] * wq;
+        wm[q * G + g] = wq;
+      }
+      gm[g] = Mn;
+      gm[kMaxGroup + g] = L;
+      gm[2 * kMaxGroup + g] = so;
+    }
+    __syncthreads();
+    const float* acl = (const float*)accl;
+    for (int e = 0; e < ept; ++e) {
+      const int idx = tid + e * NT;
+      if (idx < GD) {
+        const int g = idx / D;
+        float a = accv[e] * gm[2 * kMaxGroup + g];
+#pragma unroll 8
+        for (int q = 0; q < nq; ++q) a += acl[q * GD + idx] * wm[q * G + g];
+        accv[e] = a;
+      }
+    }
+    __syncthreads();
+  }
+  for (int e = 0; e < ept; ++e) {
+    const int idx = tid + e * NT;
+    if (idx < GD) Elem<T>::store(o, idx, accv[e] / gm[kMaxGroup + idx / D]);
+  }
+}
 
 // Merge the NW wave states in LDS (layout: ml[w][g] = (m, l),
 // acc[w][g][d]), then either write the final output (whole segment) or a
@@ -209,8 +322,8 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // moved, so its agent-coherent loads see them.  It resets the counter for
 // the next launch.
 template <typename T, int NT, int NW>
-__device__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Piece& pc, int s,
-                             float* mrg_ml, float* mrg_acc) {
+__device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Piece& pc, int s,
+                                             float* mrg_ml, float* mrg_acc, uint8_t* lds, int lds_bytes) {
   const int tid = threadIdx.x;
   const int G = p.G;
   const int GD = G * D;
@@ -256,9 +369,9 @@ __device__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Pie
   }
   wait_vmem();
   __syncthreads();
-  const int64_t Tt = sl.T, P = sl.P;
-  const int64_t p_first = min(max(owner_of(pc.seg_lo, Tt, P), (int64_t)0), P - 1);
-  const int64_t p_last = min(max(owner_of(pc.seg_hi - 1, Tt, P), p_first), P - 1);
+  const int64_t R = sl.R, P = sl.P;
+  const int64_t p_first = min(max(owner_of(pc.seg_base, R, P), (int64_t)0), P - 1);
+  const int64_t p_last = min(max(owner_of(pc.seg_base + pc.seg_len - 1, R, P), p_first), P - 1);
   if (tid == 0) {
     const int old = __hip_atomic_fetch_add(&p.counters[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     sl.is_last = (old == (int)(p_last - p_first));
@@ -269,60 +382,7 @@ __device__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Pie
   T* o = (T*)p.out + (int64_t)s * GD;
   const int np = (int)(p_last - p_first + 1);
   const int64_t s0 = p_first + s;  // slot of the first piece
-  // The merge area is free now; it holds the per-piece (m, l) and then the
-  // per-piece weights exp2(m_q - M) / L, so the accumulator pass below has
-  // no dependent loads and keeps many of them in flight.
-  const int cap = NW * kMaxGroup * D;
-  if (2 * np * G + 2 * G <= cap) {
-    float* wm = mrg_acc;               // [np][G] m, then weights
-    float* wl = mrg_acc + np * G;      // [np][G] l
-    float* gm = mrg_acc + 2 * np * G;  // [G] max, [G] 1 / sum
-    for (int j = tid; j < np * G; j += NT) {
-      const int64_t sq = s0 + j / G;
-      const int g = j % G;
-      wm[j] = ld_agent(p.part_ml + (sq * G + g) * 2);
-      wl[j] = ld_agent(p.part_ml + (sq * G + g) * 2 + 1);
-    }
-    __syncthreads();
-    for (int g = tid; g < G; g += NT) {
-      float M = kNegBig;
-      for (int q = 0; q < np; ++q) M = fmaxf(M, wm[q * G + g]);
-      float L = 0.f;
-      for (int q = 0; q < np; ++q) L += wl[q * G + g] * exp2f(wm[q * G + g] - M);
-      gm[g] = M;
-      gm[G + g] = 1.f / L;
-    }
-    __syncthreads();
-    for (int j = tid; j < np * G; j += NT) {
-      const int g = j % G;
-      wm[j] = exp2f(wm[j] - gm[g]) * gm[G + g];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < GD; idx += NT) {
-      const int g = idx / D;
-      float A = 0.f;
-#pragma unroll 8
-      for (int q = 0; q < np; ++q) A += wm[q * G + g] * ld_agent(p.part_acc + (s0 + q) * GD + idx);
-      Elem<T>::store(o, idx, A);
-    }
-  } else {
-    for (int idx = tid; idx < GD; idx += NT) {
-      const int g = idx / D;
-      float M = kNegBig, L = 0.f, A = 0.f;
-      for (int q = 0; q < np; ++q) {
-        const int64_t sq = s0 + q;
-        const float mq = ld_agent(p.part_ml + (sq * G + g) * 2);
-        const float lq = ld_agent(p.part_ml + (sq * G + g) * 2 + 1);
-        const float aq = ld_agent(p.part_acc + sq * GD + idx);
-        const float mn = fmaxf(M, mq);
-        const float so = exp2f(M - mn), sn = exp2f(mq - mn);
-        L = L * so + lq * sn;
-        A = A * so + aq * sn;
-        M = mn;
-      }
-      Elem<T>::store(o, idx, A / L);
-    }
-  }
+  combine_pieces<T, NT>(p, D, s0, np, o, lds, lds_bytes);
   if (tid == 0) __hip_atomic_store(&p.counters[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
 }
@@ -342,7 +402,6 @@ __device__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Pie
 // of the V rows (row pitch 288 B keeps the transposed u16 reads free of bank
 // conflicts).  The accumulator lane (q, g) holds O[g][16t + 4q + i], so the
 // online-softmax rescale by alpha[g] stays in-lane.
-static constexpr int kVPitch = 288;  // bytes per staged V row
 static constexpr int kStepRows = 32;
 
 template <typename T>
@@ -368,48 +427,89 @@ struct MfmaOps<f16_t> {
 
 template <int D, int NW>
 struct MfmaLds {
-  static constexpr int kStage = NW * kStepRows * kVPitch;
+  static constexpr int kStep = kStepRows * D * 2;  // one staged step of V
+  static constexpr int kStage = NW * 2 * kStep;     // two per wave
   static constexpr int kMerge = NW * kMaxGroup * (D + 2) * 4;
   static constexpr int kBytes = kStage > kMerge ? kStage : kMerge;
 };
 
+
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
   constexpr int NT = NW * 64;
-  constexpr int NC = D / 32;  // QK k-chunks
-  constexpr int NTD = D / 16; // PV output tiles
+  constexpr int NC = D / 32;            // QK k-chunks
+  constexpr int NTD = D / 16;           // PV output tiles
+  constexpr int CPR = D / 8;            // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;         // rows per wave-wide LDS load
+  constexpr int VO = kStepRows / RPI;   // V load instructions per step
+  constexpr int KO = 2 * NC;            // K load instructions per step
+  constexpr int VSTEP = MfmaLds<D, NW>::kStep;
   __shared__ SchedLds sl;
   __shared__ __attribute__((aligned(16))) uint8_t lds[MfmaLds<D, NW>::kBytes];
 
-  schedule<T, NT>(p, D, sl);
-  if (sl.s_first > sl.s_last) return;
-
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
   const int lane = tid & 63;
   const int lq = lane >> 4;   // lane quarter
   const int lc = lane & 15;   // lane column (g for S/P, m for MFMA A rows)
-  const int G = p.G;
   // K row of this lane inside a 16-row tile (rows permuted so that lane
   // quarter q ends up with rows 4i + q of the tile in the S output).
   const int krow = (lc & 3) * 4 + (lc >> 2);
-  uint8_t* vst = lds + w * kStepRows * kVPitch;
+  uint8_t* vbuf0 = lds + w * 2 * VSTEP;
+  uint8_t* vbuf1 = vbuf0 + VSTEP;
+  const WNW_GLOBAL uint16_t* kp = gptr<uint16_t>(p.k);
+  const WNW_GLOBAL uint16_t* vp = gptr<uint16_t>(p.v);
 
-  for (int s = sl.s_first; s <= sl.s_last; ++s) {
-    Piece pc = make_piece(p, sl, s);
-    if (pc.skip) continue;  // workgroup-uniform
-    if (pc.nrows < 0) {
-      if (tid == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
-      pc.nrows = 0;
+  // Loads address a uniform base (SGPRs) plus a 32-bit per-lane offset, so
+  // they use the scalar-base form and keep few VGPRs.
+  // K: two register buffers per wave (MFMA A layout, straight from memory).
+  auto issue_k = [&](u32x4 (&kb)[2][NC], const WNW_GLOBAL uint16_t* base, int row0, int valid) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int r = 16 * h + krow;
+      r = r < valid ? r : valid - 1;
+      const uint32_t off = (uint32_t)(row0 + r) * D + 8 * lq;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        kb[h][c] = __builtin_nontemporal_load((const WNW_GLOBAL u32x4*)(base + off + 32 * c));
     }
+  };
+  // V: two LDS buffers per wave, filled by direct global->LDS loads.  Row r
+  // is stored row-major with its 16-byte chunks XOR-swizzled by 2 * (r % 4),
+  // so the transposed reads below (four consecutive rows per lane quarter)
+  // hit distinct banks without padding.
+  auto issue_v = [&](uint8_t* vb, const WNW_GLOBAL uint16_t* base, int row0, int valid) {
+#pragma unroll
+    for (int u = 0; u < VO; ++u) {
+      const int r = u * RPI + lane / CPR;
+      const int c = (lane % CPR) ^ (2 * (r & 3));
+      const int rr = r < valid ? r : valid - 1;
+      const uint32_t off = (uint32_t)(row0 + rr) * D + 8 * c;
+      __builtin_amdgcn_global_load_lds(base + off, vb + u * 1024, 16, 0, 2 /* nt */);
+    }
+  };
+
+  // Offsets first, then q, then the K/V stream: the small loads every later
+  // step depends on are queued ahead of the bulk traffic, not behind it.
+  schedule<T, NT>(p, D, sl);
+  if (sl.s_first > sl.s_last) return;
+  const int G = p.G;
+
+  const int s_first = uni(sl.s_first), s_last = uni(sl.s_last);
+  for (int s = s_first; s <= s_last; ++s) {
+    const Piece pc = make_piece(p, sl, s);
+    if (pc.skip) continue;  // workgroup-uniform
+    const int nsteps = (pc.nrows + kStepRows - 1) / kStepRows;
+    auto step_rows = [&](int st) { return min(kStepRows, pc.nrows - st * kStepRows); };
+    u32x4 kA[2][NC], kB[2][NC];
     // q^T operand: lane (lq, lc) holds q[g = lc][32c + 8lq .. +8].
     u32x4 qb[NC];
     {
-      const uint16_t* qs = (const uint16_t*)p.q + (int64_t)s * G * D;
+      const WNW_GLOBAL uint16_t* qs = gptr<uint16_t>(p.q) + (int64_t)s * G * D;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         if (lc < G)
-          qb[c] = *(const u32x4*)(qs + lc * D + 32 * c + 8 * lq);
+          qb[c] = *(const WNW_GLOBAL u32x4*)(qs + lc * D + 32 * c + 8 * lq);
         else
           qb[c] = u32x4{0, 0, 0, 0};
       }
@@ -419,46 +519,29 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
 #pragma unroll
     for (int t = 0; t < NTD; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nsteps = (pc.nrows + kStepRows - 1) / kStepRows;
-    const uint16_t* kp = (const uint16_t*)p.k;
-    const uint16_t* vp = (const uint16_t*)p.v;
+    // piece base pointers (uniform); row offsets within a piece fit in 32 bits
+    const WNW_GLOBAL uint16_t* kpc = kp + pc.phys * D;
+    const WNW_GLOBAL uint16_t* vpc = vp + pc.phys * D;
+    __builtin_amdgcn_sched_barrier(0);
+    if (w < nsteps) {
+      issue_k(kA, kpc, w * kStepRows, step_rows(w));
+      issue_v(vbuf0, vpc, w * kStepRows, step_rows(w));
+    }
+    if (w + NW < nsteps) {
+      issue_k(kB, kpc, (w + NW) * kStepRows, step_rows(w + NW));
+      issue_v(vbuf1, vpc, (w + NW) * kStepRows, step_rows(w + NW));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
-    u32x4 kb[2][NC];
-    u32x4 vb[kStepRows * D / 8 / 64];  // 16-byte chunks per lane
-    constexpr int VCH = kStepRows * D / 8 / 64;
-    constexpr int CPR = D / 8;          // chunks per row
-    constexpr int RPI = 64 / CPR;       // rows per wave instruction
-
-    auto issue_loads = [&](int step) {
-      const int64_t r0 = pc.phys + (int64_t)step * kStepRows;
-      const int valid = min(kStepRows, pc.nrows - step * kStepRows);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int r = 16 * h + krow;
-        r = r < valid ? r : valid - 1;
-        const uint16_t* rowp = kp + (r0 + r) * D + 8 * lq;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) kb[h][c] = __builtin_nontemporal_load((const u32x4*)(rowp + 32 * c));
-      }
-#pragma unroll
-      for (int u = 0; u < VCH; ++u) {
-        int r = u * RPI + lane / CPR;
-        r = r < valid ? r : valid - 1;
-        vb[u] = __builtin_nontemporal_load((const u32x4*)(vp + (r0 + r) * D + 8 * (lane % CPR)));
-      }
-    };
-
-    int step = w;
-    if (step < nsteps) issue_loads(step);
-    for (; step < nsteps; step += NW) {
-      const int valid = min(kStepRows, pc.nrows - step * kStepRows);
-      // stage V rows (row-major, padded pitch) for the transposed reads
-#pragma unroll
-      for (int u = 0; u < VCH; ++u) {
-        const int r = u * RPI + lane / CPR;
-        *(u32x4*)(vst + r * kVPitch + (lane % CPR) * 16) = vb[u];
-      }
-      // S^T = K q^T for the two tiles
+    // One step: QK from the K registers, refill them two steps ahead,
+    // softmax, wait for this step's V, PV from LDS, refill the V buffer two
+    // steps ahead.  In-order issue (pinned by sched_barrier) makes the number
+    // of vector-memory ops issued after this step's V loads exactly
+    // (KO + VO) * has1 + KO * has2, which is what the wait allows in flight.
+    auto process = [&](u32x4 (&kb)[2][NC], uint8_t* vb, int st) {
+      const int valid = step_rows(st);
+      const bool has1 = st + NW < nsteps;
+      const bool has2 = st + 2 * NW < nsteps;
       f32x4 sacc[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -466,8 +549,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) sacc[h] = MfmaOps<T>::mma(kb[h][c], qb[c], sacc[h]);
       }
-      const int nstep = step + NW;
-      if (nstep < nsteps) issue_loads(nstep);
+      __builtin_amdgcn_sched_barrier(0);
+      if (has2) issue_k(kb, kpc, (st + 2 * NW) * kStepRows, step_rows(st + 2 * NW));
+      __builtin_amdgcn_sched_barrier(0);
 
       // online softmax for g = lc over the 8 rows this lane holds
       float sv[2][4];
@@ -510,15 +594,27 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
         bl[j] = plo[0][2 * j] | (plo[0][2 * j + 1] << 16);
         bl[2 + j] = plo[1][2 * j] | (plo[1][2 * j + 1] << 16);
       }
-      // O^T += V^T P^T, V^T read transposed from the staged rows
+      __builtin_amdgcn_sched_barrier(0);
+      if (has1) {
+        if (has2)
+          wait_vmcnt<2 * KO + VO>();
+        else
+          wait_vmcnt<KO + VO>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // O^T += V^T P^T, V^T read transposed from the staged rows: element
+      // (row r, dim d) is at r * 2D + ((d / 8) ^ (2 (r % 4))) * 16 + (d % 8) * 2,
+      // and every row this lane reads has r % 4 == lq.
 #pragma unroll
       for (int t = 0; t < NTD; ++t) {
-        const uint8_t* col = vst + (16 * t + lc) * 2;
+        const uint8_t* col = vb + (((2 * t + (lc >> 3)) ^ (2 * lq)) * 16) + (lc & 7) * 2;
         uint32_t e[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int r = (j < 4) ? (4 * j + lq) : (16 + 4 * (j - 4) + lq);
-          e[j] = *(const uint16_t*)(col + r * kVPitch);
+          e[j] = *(const uint16_t*)(col + r * (2 * D));
         }
         u32x4 a;
 #pragma unroll
@@ -526,6 +622,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
         acc[t] = MfmaOps<T>::mma(a, bh, acc[t]);
         acc[t] = MfmaOps<T>::mma(a, bl, acc[t]);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (has2) issue_v(vb, vpc, (st + 2 * NW) * kStepRows, step_rows(st + 2 * NW));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    for (int st = w; st < nsteps; st += 2 * NW) {
+      process(kA, vbuf0, st);
+      if (st + NW < nsteps) process(kB, vbuf1, st + NW);
     }
     // l over the lane quarters (same g)
     l_run += swap16(l_run);
@@ -544,8 +648,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
         *(f32x4*)(mrg_acc + (w * kMaxGroup + lc) * D + 16 * t + 4 * lq) = acc[t];
     }
     __syncthreads();
-    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc);
+    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc, lds, MfmaLds<D, NW>::kBytes);
   }
+  wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -585,12 +690,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_valu_kernel(AttnParams p) {
   const T* vp = (const T*)p.v;
 
   for (int s = sl.s_first; s <= sl.s_last; ++s) {
-    Piece pc = make_piece(p, sl, s);
+    const Piece pc = make_piece(p, sl, s);
     if (pc.skip) continue;  // workgroup-uniform
-    if (pc.nrows < 0) {
-      if (tid == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
-      pc.nrows = 0;
-    }
     const T* qs = (const T*)p.q + (int64_t)s * G * D;
     for (int idx = tid; idx < G * D; idx += NT) qf[idx] = Elem<T>::to_f32(qs, idx);
     __syncthreads();
@@ -674,7 +775,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_valu_kernel(AttnParams p) {
       }
     }
     __syncthreads();
-    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc);
+    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc, lds, ValuLds<D, NW>::kBytes);
   }
 }
 
@@ -804,7 +905,7 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
   if (P <= 0) {
     // Balanced split of the rows over up to 2 workgroups per CU, never
     // fewer than ~64 rows per workgroup.
-    const int64_t by_rows = std::max<int64_t>(1, (total_rows + 63) / 64);
+    const int64_t by_rows = std::max<int64_t>(1, (kv_rows + 63) / 64);
     P = std::min<int64_t>((int64_t)di.cus * 2, by_rows);
   }
   P = std::max<int64_t>(1, std::min<int64_t>(P, di.max_wg));

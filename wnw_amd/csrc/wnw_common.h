@@ -127,4 +127,18 @@ __device__ __forceinline__ void raise_device_error(int32_t* err, int bits) {
   if (err) atomicOr(err, bits);
 }
 
+// Global-memory pointers.  Pointers that reach a kernel inside a struct are
+// generic; accessing through them emits FLAT instructions, which are slower
+// and count against both vmcnt and lgkmcnt.  Casting to address space 1 gives
+// global_* instructions with the scalar-base addressing form.
+#define WNW_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const WNW_GLOBAL T* gptr(const void* p) {
+  return (const WNW_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ WNW_GLOBAL T* gptr_w(void* p) {
+  return (WNW_GLOBAL T*)p;
+}
+
 }  // namespace wnw
