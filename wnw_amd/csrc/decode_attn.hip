@@ -231,11 +231,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Last-arriver merge of the np partials of one segment (slots s0 .. s0+np-1)
 // into the output.  The partials of consecutive slots are contiguous, so a
-// chunk of pieces is one contiguous block: it is copied straight into LDS
-// with agent-coherent (sc1) direct global->LDS loads, together with the
-// pieces' (m, l), at the cost of one memory round trip and almost no
-// registers.  Summation order is fixed, so results are deterministic.
-// `lds` / `lds_bytes` is the workgroup's LDS, free at this point.
+// chunk of pieces is one contiguous block of accumulators and one of (m, l)
+// pairs: both are copied straight into LDS with agent-coherent (sc1) direct
+// global->LDS loads, one memory round trip per chunk and almost no
+// registers.  Per head, a wave reduces the chunk's maxima and sums across
+// its lanes (one piece per lane); then every thread folds its output
+// elements over the chunk.  Summation order is fixed, so results are
+// deterministic.  `lds` / `lds_bytes` is the workgroup's LDS, free here.
 template <typename T, int NT>
 __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, T* o,
                                                uint8_t* lds, int lds_bytes) {
@@ -244,51 +246,53 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
   const int lane = tid & 63;
   const int G = p.G;
   const int GD = G * D;
-  float* gm = (float*)lds;                    // [3][16]: M, L, rescale
-  float* wm = gm + 3 * kMaxGroup;             // [pch][G] m, then weights
-  const int head = 3 * kMaxGroup * 4;         // bytes before the per-piece tables
-  // pieces per chunk: tables (8 * G bytes each) + accumulators (4 * GD bytes each)
-  const int room = (lds_bytes - head - 1024) / (4 * GD + 8 * G);
-  const int pch = max(1, min(np, room));
-  float* wl = wm + pch * G;                   // [pch][G] l
-  uint8_t* accl = (uint8_t*)(((uintptr_t)(wl + pch * G) + 1023) & ~(uintptr_t)1023);  // [pch][GD]
+  float* gm = (float*)lds;                    // [3][16]: M, L, rescale per head
+  float* wml = gm + 3 * kMaxGroup;            // [pch][G][2]: (m, l), then (weight, l)
+  const int head = 3 * kMaxGroup * 4;         // bytes before the (m, l) table
+  // pieces per chunk (at most one per lane): (m, l) table (8 * G bytes each)
+  // + accumulators (4 * GD bytes each), 1 KB of alignment slack
+  const int room = (lds_bytes - head - 2048) / (4 * GD + 8 * G);
+  const int pch = max(1, min(min(np, room), 64));
+  // 1 KB aligned.  The offset is rounded as an integer so that the pointer
+  // keeps its LDS address space (a round trip through uintptr_t would make
+  // every access a FLAT one, which forces full memory waits).
+  uint8_t* accl = lds + ((head + 8 * pch * G + 1023) & ~1023);  // [pch][GD]
   const int ept = (GD + NT - 1) / NT;
   float accv[kMaxGroup * 256 / 256];          // up to 16 elements per thread (G * D <= 4096)
 #pragma unroll
   for (int e = 0; e < kMaxGroup * 256 / 256; ++e) accv[e] = 0.f;
   for (int q0 = 0; q0 < np; q0 += pch) {
     const int nq = min(pch, np - q0);
-    // accumulators: nq * GD floats, contiguous, 1 KB per wave-wide load
+    // accumulators: nq * GD floats, 1 KB per wave-wide 16-byte load
     const int nvec = nq * GD / 4;
     const WNW_GLOBAL float* src = gptr<float>(p.part_acc + (s0 + q0) * GD);
     for (int k = w; k * 64 < nvec; k += NT / 64) {
       const int v = k * 64 + lane;
-      if (v < nvec) __builtin_amdgcn_global_load_lds(src + 4 * v, accl + k * 1024, 16, 0, 16);
+      if (v < nvec) __builtin_amdgcn_global_load_lds(src + 4 * v, accl + k * 1024, 16, 0, 16 /* sc1 */);
     }
-    for (int j = tid; j < nq * G; j += NT) {
-      const int64_t sq = s0 + q0 + j / G;
-      const int g = j % G;
-      wm[j] = ld_agent(p.part_ml + (sq * G + g) * 2);
-      wl[j] = ld_agent(p.part_ml + (sq * G + g) * 2 + 1);
+    // (m, l) pairs: nq * G * 2 floats, 256 B per wave-wide 4-byte load
+    const int nml = nq * G * 2;
+    const WNW_GLOBAL float* srcm = gptr<float>(p.part_ml + (s0 + q0) * G * 2);
+    for (int k = w; k * 64 < nml; k += NT / 64) {
+      const int v = k * 64 + lane;
+      if (v < nml) __builtin_amdgcn_global_load_lds(srcm + v, (uint8_t*)wml + k * 256, 4, 0, 16 /* sc1 */);
     }
     wait_vmcnt<0>();
     __syncthreads();
-    if (tid < G) {  // running max and sum per head, rescale of what is merged so far
-      const int g = tid;
+    // wave w takes heads w, w + NW, ...; lane q holds piece q of the chunk
+    for (int g = w; g < G; g += NT / 64) {
       const float M = q0 == 0 ? kNegBig : gm[g];
-      float L = q0 == 0 ? 0.f : gm[kMaxGroup + g];
-      float Mn = M;
-      for (int q = 0; q < nq; ++q) Mn = fmaxf(Mn, wm[q * G + g]);
-      const float so = exp2f(M - Mn);
-      L *= so;
-      for (int q = 0; q < nq; ++q) {
-        const float wq = exp2f(wm[q * G + g] - Mn);
-        L += wl[q * G + g] * wq;
-        wm[q * G + g] = wq;
+      const float mq = lane < nq ? wml[(lane * G + g) * 2] : kNegBig;
+      const float Mn = fmaxf(M, wave_max(mq));
+      const float wq = lane < nq ? exp2f(mq - Mn) : 0.f;
+      const float lsum = wave_sum(lane < nq ? wml[(lane * G + g) * 2 + 1] * wq : 0.f);
+      if (lane < nq) wml[(lane * G + g) * 2] = wq;
+      if (lane == 0) {
+        const float so = exp2f(M - Mn);
+        gm[kMaxGroup + g] = (q0 == 0 ? 0.f : gm[kMaxGroup + g]) * so + lsum;
+        gm[2 * kMaxGroup + g] = so;
+        gm[g] = Mn;
       }
-      gm[g] = Mn;
-      gm[kMaxGroup + g] = L;
-      gm[2 * kMaxGroup + g] = so;
     }
     __syncthreads();
     const float* acl = (const float*)accl;
@@ -298,7 +302,7 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
         const int g = idx / D;
         float a = accv[e] * gm[2 * kMaxGroup + g];
 #pragma unroll 8
-        for (int q = 0; q < nq; ++q) a += acl[q * GD + idx] * wm[q * G + g];
+        for (int q = 0; q < nq; ++q) a += acl[q * GD + idx] * wml[(q * G + g) * 2];
         accv[e] = a;
       }
     }
