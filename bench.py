@@ -20,8 +20,12 @@ Reported:
                     events around back-to-back attention-only graph replays.
 * roofline       -- the attention kernel: algorithmic bytes per launch /
                     average launch time vs 8 TB/s.
+* append_us_per_layer_step -- the in-place append kernel alone, per layer-step.
 * cpu_baseline   -- the float64 C oracle (1 core) on a bounded sample of the
                     same layers.
+
+``--copy-calibration`` only runs a plain 256 MiB device-to-device copy three
+times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes).
 """
 from __future__ import annotations
 
@@ -50,7 +54,25 @@ def parse():
                     help="layers timed for the CPU baseline (0 = choose ~15 s of work)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy three times (PMC byte calibration)")
     return ap.parse_args()
+
+
+COPY_CAL_BYTES = 256 << 20
+
+
+def copy_calibration():
+    """A plain copy kernel of known size: reads and writes COPY_CAL_BYTES each."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    a = torch.ones(COPY_CAL_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_CAL_BYTES, "launches": 3}), flush=True)
 
 
 class LayerState:
@@ -94,6 +116,9 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the decode path is single-GPU "
               "per process and multi-GPU runs are not part of this build", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import numpy as np
     import torch
@@ -113,7 +138,8 @@ def main():
     gen.manual_seed(0)
     print(f"# config {cfg.name}: layers={L} n_seg={N} G={G} D={D} steps={args.steps} warmup={args.warmup}",
           flush=True)
-    layers = [LayerState(cfg, l, total_steps + 2, dev, gen) for l in range(L)]
+    # slack: one row per step, plus the four appends of the append-only timing
+    layers = [LayerState(cfg, l, total_steps + 6, dev, gen) for l in range(L)]
     torch.cuda.synchronize()
     ws = fused_attn.AttnWorkspace(dev)
     ws.get(N, G, D)
@@ -126,6 +152,10 @@ def main():
             fused_attn.decode_attn(st.q, st.k, st.v, cu_new, scale, seg_base=st.base, total_rows=st.pool_rows,
                                    out=st.out, workspace=ws, kernel=args.kernel)
 
+    def append_launches(parity: int):
+        for st in layers:
+            append_inplace(st.k, st.v, st.new_k, st.new_v, st.cu[parity], st.cu[1 - parity], st.base, st.cap)
+
     def attn_launches():
         for st in layers:
             fused_attn.decode_attn(st.q, st.k, st.v, st.cu[0], scale, seg_base=st.base, total_rows=st.pool_rows,
@@ -134,6 +164,7 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     graphs = None
     attn_graph = None
+    append_graphs = None
     if not args.no_graph:
         # capture on a side stream (default priority), then replay
         with torch.cuda.stream(stream):
@@ -148,6 +179,12 @@ def main():
         attn_graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(attn_graph, stream=stream):
             attn_launches()
+        append_graphs = []
+        for parity in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                append_launches(parity)
+            append_graphs.append(g)
         torch.cuda.synchronize()
         for st in layers:  # capture does not execute; start from the initial offsets
             st.reset()
@@ -214,6 +251,24 @@ def main():
     achieved_gbs = avg_bytes / (us_per_launch * 1e-6) / 1e9
     assert _lib.device_error() == 0, "device error during attention timing"
 
+    # ---- append-only kernel timing: two appends (there and back) per rep --
+    # The slack leaves room for them: rows stay within each segment's capacity.
+    app_reps = 2
+    with torch.cuda.stream(stream):
+        ev2 = torch.cuda.Event(enable_timing=True)
+        ev3 = torch.cuda.Event(enable_timing=True)
+        ev2.record(stream)
+        for r in range(app_reps):
+            for parity in (0, 1):
+                if append_graphs is not None:
+                    append_graphs[parity].replay()
+                else:
+                    append_launches(parity)
+        ev3.record(stream)
+        ev3.synchronize()
+    append_us = ev2.elapsed_time(ev3) * 1e3 / (2 * app_reps * L)
+    assert _lib.device_error() == 0, "device error during append timing"
+
     # ---- CPU baseline: float64 C oracle on a bounded sample ---------------
     cpu = None
     if not args.no_cpu:
@@ -236,6 +291,7 @@ def main():
                    "head_dim": D, "n_seg": N, "rows_per_layer_step": int(np.mean(rows_attn)),
                    "kernel": args.kernel, "graph": graphs is not None, "notes": cfg.notes},
         "us_per_layer_step": round(us_per_launch, 3),
+        "append_us_per_layer_step": round(append_us, 3),
         "attn_TBs": round(achieved_gbs / 1e3, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name)},
