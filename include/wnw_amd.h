@@ -42,7 +42,8 @@ extern "C" {
 
 /* device error bits recorded by kernels (wnw_device_error) */
 #define WNW_DEVERR_BOUNDS 1   /* an offset pointed outside the given rows  */
-#define WNW_DEVERR_ORDER 2    /* cu_seqlens not non-decreasing             */
+#define WNW_DEVERR_ORDER 2    /* cu_seqlens decreasing, or segments not in
+                                 index order in the physical rows         */
 #define WNW_DEVERR_CAPACITY 4 /* in-place append beyond segment capacity   */
 
 /* attention kernel selection (wnw_decode_attn_ex) */
@@ -194,8 +195,14 @@ int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
  * where q is [n_seg, group, head_dim] (q head h = kv * group + g,
  * session.py:81-83) and K_s/V_s are the rows of segment s.  fp32 softmax
  * and accumulation; out has the dtype of q/K/V.  An empty segment yields
- * zeros.  total_rows is an upper bound of cu_k[n_seg] (it only sizes the
- * grid); kv_rows is the number of rows allocated in k and v.
+ * zeros.  kv_rows is the number of rows allocated in k and v: the kernel
+ * splits this physical row range evenly over its workgroups, so the cost
+ * does not depend on how ragged the segments are.  Segments must be laid
+ * out in index order (seg_base[s] + len[s] <= seg_base[s+1]; the dense
+ * layout, seg_base NULL, always is); a violation sets WNW_DEVERR_ORDER and
+ * a segment outside [0, kv_rows) sets WNW_DEVERR_BOUNDS and yields NaN.
+ * total_rows (an upper bound of cu_k[n_seg]) is checked for sign only and
+ * kept for signature stability.
  */
 int wnw_decode_attn(const void* q, const void* k, const void* v,
                     const int32_t* cu_k, const int64_t* seg_base,
@@ -216,6 +223,81 @@ int wnw_decode_attn_ex(const void* q, const void* k, const void* v,
                        int dtype, void* out, void* workspace,
                        int64_t workspace_bytes, int kernel, int64_t n_wg,
                        void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Host planner (CPU only; no HIP calls)                                     */
+/* ------------------------------------------------------------------------ */
+/*
+ * Replaces the reference's pybind `Planner` class (src/algorithms/wnw_cpp/
+ * code/planner.cpp:16-341; methods bound at :327-341) one call for one
+ * method.  It turns each step's top-k chunk lists into the compaction
+ * descriptors of wnw_rebuild_append_kv for every layer and gathers the
+ * host rows to load into pinned staging.  Arrays are caller-owned int32;
+ * "flattened" means row-major over the listed dimensions.  The planner keeps
+ * raw pointers to the restore and staging buffers (caller keeps them alive).
+ */
+typedef struct wnw_planner wnw_planner;
+
+/* Planner(L, H, B, G) (planner.cpp:18-25); NULL on bad dimensions. */
+wnw_planner* wnw_planner_create(int num_layers, int num_kv_heads,
+                                int batch_size, int group);
+void wnw_planner_destroy(wnw_planner* p);
+/* set_config (planner.cpp:27-30) */
+int wnw_planner_set_config(wnw_planner* p, int top_k_chunks, int eviction_lag);
+/* set_seg_count (planner.cpp:32): segments per sample, n = batch */
+int wnw_planner_set_seg_count(wnw_planner* p, const int32_t* seg_count,
+                              int64_t n);
+/* set_chunk_to_segs (planner.cpp:34-42): CSR of chunk -> segments, sample b */
+int wnw_planner_set_chunk_to_segs(wnw_planner* p, int b,
+                                  const int32_t* flat_segs,
+                                  const int32_t* offsets, int64_t num_chunks);
+/* set_class_b (planner.cpp:44-48): class-B KV heads of one layer */
+int wnw_planner_set_class_b(wnw_planner* p, int layer, const int32_t* kv_heads,
+                            int64_t n);
+/* set_restore_meta (planner.cpp:50-77): flattened [L][B*H][segments of the
+ * sample]; host rows [cpu_s, cpu_e) and resident relative rows [gpu_s,
+ * gpu_e) of each offloaded segment, -1 = none / not resident */
+int wnw_planner_set_restore_meta(wnw_planner* p, const int32_t* cpu_s,
+                                 const int32_t* cpu_e, const int32_t* gpu_s,
+                                 const int32_t* gpu_e, int64_t n);
+/* set_loaded (planner.cpp:79-84) */
+int wnw_planner_set_loaded(wnw_planner* p, int b, const int32_t* segs,
+                           int64_t n);
+/* set_seq_lens (planner.cpp:86-95): flattened [L][B*H] segment lengths;
+ * resets the eviction counters */
+int wnw_planner_set_seq_lens(wnw_planner* p, const int32_t* lens, int64_t n);
+/* get_loaded_segments (planner.cpp:97-99): writes up to cap ascending
+ * segment ids, returns the count (-1 on error) */
+int64_t wnw_planner_get_loaded_segments(wnw_planner* p, int b, int32_t* out,
+                                        int64_t cap);
+/* set_restore_buffers (planner.cpp:101-108): host rows and pinned staging,
+ * row_bytes = head_dim * element size */
+int wnw_planner_set_restore_buffers(wnw_planner* p, const void* cpu_k,
+                                    const void* cpu_v, void* stg_k,
+                                    void* stg_v, int64_t cpu_rows,
+                                    int64_t stg_rows, int64_t row_bytes);
+/* gather_restore (planner.cpp:113-122): copies the last plan's host ranges,
+ * in transfer order, to the start of staging (bounds-checked) */
+int wnw_planner_gather_restore(wnw_planner* p);
+/*
+ * compute_and_prepare (planner.cpp:124-306).  topk_idx/topk_off: CSR of the
+ * chosen chunks per sample (B + 1 offsets).  Writes [L][N] load_starts,
+ * load_lens, new_lens, [L][N+1] cu_new and evict_offsets (per-layer CSR),
+ * [L] evict_max and [L+1] evict_layer_ptr (into the global evict list),
+ * *any_change, *total_rows (rows to transfer), *n_evict and *n_ranges.  The
+ * evict list and the host ranges are read with the two calls below.
+ */
+int wnw_planner_compute_and_prepare(
+    wnw_planner* p, const int32_t* topk_idx, const int32_t* topk_off,
+    int32_t* load_starts_2d, int32_t* load_lens_2d, int32_t* cu_new_2d,
+    int32_t* new_lens_2d, int32_t* evict_offsets_2d, int32_t* evict_max,
+    int32_t* evict_layer_ptr, int32_t* any_change, int64_t* total_rows,
+    int64_t* n_evict, int64_t* n_ranges);
+/* The (ev_s, ev_e) tensors of compute_and_prepare's result tuple */
+int wnw_planner_get_evictions(wnw_planner* p, int32_t* starts, int32_t* ends,
+                              int64_t cap);
+/* The `ranges` [n, 2] tensor of compute_and_prepare's result tuple */
+int wnw_planner_get_ranges(wnw_planner* p, int32_t* ranges, int64_t cap);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,22 @@ _SIGNATURES = {
                                _i64, _vp]),
     "wnw_decode_attn_ex": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp, _vp,
                                   _i64, _i32, _i64, _vp]),
+    # host planner (CPU only)
+    "wnw_planner_create": (_vp, [_i32, _i32, _i32, _i32]),
+    "wnw_planner_destroy": (None, [_vp]),
+    "wnw_planner_set_config": (_i32, [_vp, _i32, _i32]),
+    "wnw_planner_set_seg_count": (_i32, [_vp, _vp, _i64]),
+    "wnw_planner_set_chunk_to_segs": (_i32, [_vp, _i32, _vp, _vp, _i64]),
+    "wnw_planner_set_class_b": (_i32, [_vp, _i32, _vp, _i64]),
+    "wnw_planner_set_restore_meta": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64]),
+    "wnw_planner_set_loaded": (_i32, [_vp, _i32, _vp, _i64]),
+    "wnw_planner_set_seq_lens": (_i32, [_vp, _vp, _i64]),
+    "wnw_planner_get_loaded_segments": (_i64, [_vp, _i32, _vp, _i64]),
+    "wnw_planner_set_restore_buffers": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+    "wnw_planner_gather_restore": (_i32, [_vp]),
+    "wnw_planner_compute_and_prepare": (_i32, [_vp] * 14),
+    "wnw_planner_get_evictions": (_i32, [_vp, _vp, _vp, _i64]),
+    "wnw_planner_get_ranges": (_i32, [_vp, _vp, _i64]),
 }
 
 
