@@ -225,6 +225,67 @@ int wnw_decode_attn_ex(const void* q, const void* k, const void* v,
                        void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Class-A token scores                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace of wnw_decode_attn_score: the attention workspace followed by
+ * the per-segment softmax normalisers.  Same clearing rule as the attention
+ * workspace (wnw_workspace_init once, again before a larger n_seg). */
+int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group,
+                                              int64_t head_dim);
+
+/*
+ * Decode attention + class-A score accumulation, the reference's
+ * q1_decode_attn_score (src/common/kv/fused_attn.py:68-156, used for
+ * "foldable" layers by WnWCache.fused_decode_attention, src/algorithms/wnw/
+ * code/cache.py:546-566).  out is wnw_decode_attn's result.  Then, for every
+ * segment s = b * num_kv_heads + kv with ca_kv_mask[kv] != 0 and every
+ * audio row j in [audio_starts[b], audio_ends[b]) of the segment,
+ *   score_acc[score_offsets[b] + j - audio_starts[b]] +=
+ *       sum_g exp(scale * q[s, g] . K[row j] - m[s, g]) / l[s, g]
+ * with (m, l) the final softmax max / sum of the attention itself (the
+ * reference adds with atomics; here one workgroup owns each token, so the
+ * sum is deterministic).  max_audio >= every audio_ends[b] - audio_starts[b]
+ * (it sizes the grid); acc_len = entries of score_acc.  Audio ranges outside
+ * a segment set WNW_DEVERR_BOUNDS and skip that segment.
+ */
+int wnw_decode_attn_score(const void* q, const void* k, const void* v,
+                          const int32_t* cu_k, const int64_t* seg_base,
+                          int64_t n_seg, int64_t group, int64_t head_dim,
+                          int64_t total_rows, int64_t kv_rows, float scale,
+                          int dtype, void* out, const int32_t* ca_kv_mask,
+                          int64_t num_kv_heads, const int32_t* audio_starts,
+                          const int32_t* audio_ends, float* score_acc,
+                          const int32_t* score_offsets, int64_t acc_len,
+                          int64_t max_audio, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
+/* Workspace of wnw_fused_score_accumulate (partial softmax statistics). */
+int64_t wnw_fused_score_workspace_bytes(int64_t n_samples, int64_t n_heads);
+
+/*
+ * The reference's fused_score_accumulate (src/algorithms/wnw/code/
+ * kernels.py:302-370): for each of n_samples items with query heads
+ * q[i, 0..n_heads), the softmax over K rows [seg_starts[i], seg_ends[i]) of
+ * scale * q . K (the reference uses scale = head_dim^-0.5), summed over the
+ * heads, is added at the audio rows [audio_starts[i], audio_ends[i])
+ * (relative to seg_starts[i]) to accumulator[accum_offsets[i] + j].
+ * Two launches: partial statistics over 32 row slices per item, then the
+ * scoring pass over the audio rows.  k_rows = rows of k (bounds).
+ */
+int wnw_fused_score_accumulate(const void* q, const void* k,
+                               const int32_t* seg_starts,
+                               const int32_t* seg_ends,
+                               const int32_t* audio_starts,
+                               const int32_t* audio_ends, float* accumulator,
+                               const int32_t* accum_offsets, int64_t n_samples,
+                               int64_t n_heads, int64_t head_dim,
+                               int64_t k_rows, int64_t acc_len,
+                               int64_t max_audio, float scale, int dtype,
+                               void* workspace, int64_t workspace_bytes,
+                               void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Host planner (CPU only; no HIP calls)                                     */
 /* ------------------------------------------------------------------------ */
 /*

@@ -49,8 +49,9 @@ def lib() -> ctypes.CDLL:
         l.oracle_interleave_append.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, vp]
         l.oracle_rebuild_append_kv.argtypes = [vp] * 13 + [i64] * 7 + [i32, vp, vp]
         l.oracle_rebuild_by_slices.argtypes = [vp] * 12 + [i64, i64, i32, vp, vp, vp]
+        l.oracle_segment_scores.argtypes = [vp] * 7 + [i64, i64, i64, dbl, i32, i64, i64, vp]
         for f in (l.oracle_decode_attn, l.oracle_interleave_append, l.oracle_rebuild_append_kv,
-                  l.oracle_rebuild_by_slices):
+                  l.oracle_rebuild_by_slices, l.oracle_segment_scores):
             f.restype = ctypes.c_int
         _lib = l
     return _lib
@@ -108,6 +109,39 @@ def decode_attn(q, k, v, cu, scale, base=None, dtype=None):
     if rc != 0:
         raise ValueError("oracle_decode_attn: inconsistent offsets")
     return out
+
+
+def segment_scores(q, k, r0, r1, a0, a1, off, scale, acc, dtype=None):
+    """float64 class-A scores added into ``acc`` (float64, updated in place).
+
+    q [items, nh, D]; per item: K rows [r0, r1), audio rows [a0, a1) relative
+    to r0, accumulator offset ``off``."""
+    dt = _dtype_code(q, dtype)
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    n, nh, d = q.shape
+    i64 = lambda a: np.ascontiguousarray(a, dtype=np.int64)  # noqa: E731
+    i32 = lambda a: np.ascontiguousarray(a, dtype=np.int32)  # noqa: E731
+    assert acc.dtype == np.float64 and acc.flags.c_contiguous
+    rc = lib().oracle_segment_scores(_p(q), _p(k), _p(i64(r0)), _p(i64(r1)), _p(i32(a0)), _p(i32(a1)),
+                                     _p(i64(off)), n, nh, d, float(scale), dt, k.shape[0], acc.size, _p(acc))
+    if rc != 0:
+        raise ValueError("oracle_segment_scores: inconsistent ranges")
+    return acc
+
+
+def attn_scores(q, k, cu, scale, ca_kv_mask, num_kv_heads, audio_s, audio_e, offsets, acc, base=None, dtype=None):
+    """q1_decode_attn_score's scoring part (fused_attn.py:112-123) mapped onto
+    ``segment_scores``: one item per segment whose KV head is flagged."""
+    n_seg = q.shape[0]
+    items = [s for s in range(n_seg) if ca_kv_mask[s % num_kv_heads]]
+    if not items:
+        return acc
+    bs = [s // num_kv_heads for s in items]
+    start = [int(base[s]) if base is not None else int(cu[s]) for s in items]
+    r1 = [st + int(cu[s + 1]) - int(cu[s]) for st, s in zip(start, items)]
+    return segment_scores(q[items], k, start, r1, [audio_s[b] for b in bs], [audio_e[b] for b in bs],
+                          [offsets[b] for b in bs], scale, acc, dtype=dtype)
 
 
 def interleave_append(old, new, cu_old, cu_new, dtype=None):

@@ -241,3 +241,61 @@ int oracle_rebuild_by_slices(const void* old_k, const void* old_v,
   }
   return 0;
 }
+
+/*
+ * Class-A token scores (float64).  Item i has nh query heads
+ * q[i, 0..nh) and the K rows [r0[i], r1[i]); for each head the softmax of
+ * scale * q . K over those rows is formed, and for the audio rows
+ * [r0 + a0[i], r0 + a1[i]) the weights, summed over the heads, are added to
+ * acc[off[i] + j].  This is the arithmetic of both reference scorers:
+ * q1_decode_attn_score (src/common/kv/fused_attn.py:68-123, one item per
+ * flagged segment, heads = the group) and fused_score_accumulate
+ * (src/algorithms/wnw/code/kernels.py:351-370, _fused_score_pytorch).
+ * Returns -1 on inconsistent ranges.
+ */
+int oracle_segment_scores(const void* q, const void* k, const int64_t* r0,
+                          const int64_t* r1, const int32_t* a0,
+                          const int32_t* a1, const int64_t* off,
+                          int64_t n_items, int64_t nh, int64_t D,
+                          double scale, int dtype, int64_t k_rows,
+                          int64_t acc_len, double* acc) {
+  double* w = NULL;
+  double* sc = NULL;
+  int rc = 0;
+  for (int64_t i = 0; i < n_items && rc == 0; ++i) {
+    const int64_t n = r1[i] - r0[i];
+    const int64_t na = (int64_t)a1[i] - a0[i];
+    if (n < 0 || r0[i] < 0 || r1[i] > k_rows || a0[i] < 0 || a1[i] > n || na < 0 || off[i] < 0 ||
+        off[i] + na > acc_len) {
+      rc = -1;
+      break;
+    }
+    if (na == 0) continue;
+    free(w);
+    free(sc);
+    w = (double*)calloc((size_t)na, sizeof(double));
+    sc = (double*)malloc(sizeof(double) * (size_t)n);
+    if (!w || !sc) {
+      rc = -1;
+      break;
+    }
+    for (int64_t h = 0; h < nh; ++h) {
+      const int64_t qoff = (i * nh + h) * D;
+      double mx = -INFINITY;
+      for (int64_t r = 0; r < n; ++r) {
+        double d = 0.0;
+        for (int64_t e = 0; e < D; ++e)
+          d += elem_to_f64(q, qoff + e, dtype) * elem_to_f64(k, (r0[i] + r) * D + e, dtype);
+        sc[r] = d * scale;
+        if (sc[r] > mx) mx = sc[r];
+      }
+      double l = 0.0;
+      for (int64_t r = 0; r < n; ++r) l += exp(sc[r] - mx);
+      for (int64_t j = 0; j < na; ++j) w[j] += exp(sc[a0[i] + j] - mx) / l;
+    }
+    for (int64_t j = 0; j < na; ++j) acc[off[i] + j] += w[j];
+  }
+  free(w);
+  free(sc);
+  return rc;
+}

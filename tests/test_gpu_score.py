@@ -1,0 +1,132 @@
+"""GPU parity of the class-A scorers against the float64 oracle.
+
+Scores are sums of softmax weights (fp32 on the GPU); they are held to
+|got - ref| <= 1e-6 + 1e-3 * |ref|.  The attention output of
+q1_decode_attn_score is held to the attention tolerance (2e-3 + 1e-2 |ref|).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import allclose_report, cu_from_lens, from_torch, rand_rows, to_torch
+from wnw_amd import _lib
+from wnw_amd import workloads
+from wnw_amd.kv import fused_attn
+from wnw_amd.wnw import kernels as wk
+
+pytestmark = pytest.mark.gpu
+
+S_ATOL, S_RTOL = 1e-6, 1e-3
+
+
+def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_rows=None, kv_scale=1.0):
+    rng = np.random.default_rng(seed)
+    n = len(lens)
+    B = n // H
+    cu = cu_from_lens(lens)
+    rows = int(cu[-1]) if pool_rows is None else pool_rows
+    q = rand_rows(rng, n * G, D, "bfloat16").reshape(n, G, D)
+    k = rand_rows(rng, rows, D, "bfloat16", kv_scale)
+    v = rand_rows(rng, rows, D, "bfloat16", kv_scale)
+    offs = np.concatenate([[0], np.cumsum(np.array(a_e) - np.array(a_s))]).astype(np.int32)
+    acc0 = rng.random(int(offs[-1])).astype(np.float32)
+    scale = D ** -0.5
+    ref_out = oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=oracle.DT_BF16)
+    ref_acc = oracle.attn_scores(q, k, cu, scale, mask, H, a_s, a_e, offs, acc0.astype(np.float64),
+                                 base=base, dtype=oracle.DT_BF16)
+    t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
+    acc = torch.from_numpy(acc0).to(dev)
+    print(f"attn_score n_seg={n} H={H} G={G} D={D} mask={mask} seed={seed}", flush=True)
+    out = fused_attn.q1_decode_attn_score(
+        to_torch(q, "bfloat16", dev), to_torch(k, "bfloat16", dev), to_torch(v, "bfloat16", dev), t(cu), scale,
+        t(mask), H, t(a_s), t(a_e), acc, t(offs),
+        seg_base=None if base is None else t(base, torch.int64), max_audio=int(max(np.array(a_e) - np.array(a_s))))
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    got_out = oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16)
+    return got_out, ref_out, acc.cpu().numpy().astype(np.float64), ref_acc
+
+
+def test_attn_score_small():
+    lens = [40, 300, 17, 1000, 64, 2, 513, 90]  # B = 2, H = 4
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 4, 4, 128, [0, 1, 0, 1],
+                                            [3, 0], [17, 2], seed=1)
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+def test_attn_score_slack_layout_and_group7():
+    lens = [500, 33, 260, 70]  # B = 2, H = 2
+    caps = [520, 40, 300, 80]
+    base = np.zeros(4, np.int64)
+    pos = 5
+    for s in range(4):
+        base[s] = pos
+        pos += caps[s] + 3
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 2, 7, 128, [1, 0], [10, 5],
+                                            [480, 250], seed=2, base=base, pool_rows=pos + 4)
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+def test_attn_score_cfg2_layer():
+    """One cfg2 layer at full size: class-A segments hold 7,500 audio rows."""
+    cfg = workloads.config2()
+    lens = cfg.lengths[0] + 1
+    H = cfg.hkv
+    mask = cfg.class_a[0].astype(np.int32).tolist()
+    a_s, a_e = [0] * cfg.batch, [7500] * cfg.batch
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, cfg.group, cfg.head_dim, mask,
+                                            a_s, a_e, seed=3, kv_scale=float(cfg.kv_scale[0].mean()))
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    print(msg)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("nh,D", [(1, 128), (4, 128), (3, 64), (2, 256)])
+def test_fused_score_accumulate(nh, D):
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(10 + nh)
+    lens = [900, 33, 5000, 1]
+    S = len(lens)
+    starts = np.concatenate([[7], 7 + np.cumsum(lens)[:-1] + 11])  # gaps between items
+    ends = starts + lens
+    rows = int(ends[-1]) + 9
+    k = rand_rows(rng, rows, D, "bfloat16")
+    q = rand_rows(rng, S * nh, D, "bfloat16").reshape(S, nh, D)
+    a_s = np.array([100, 0, 2500, 0], np.int32)
+    a_e = np.array([800, 33, 5000, 1], np.int32)
+    offs = np.concatenate([[0], np.cumsum(a_e - a_s)]).astype(np.int32)
+    acc0 = rng.random(int(offs[-1])).astype(np.float32)
+    ref = oracle.segment_scores(q, k, starts, ends, a_s, a_e, offs[:-1], D ** -0.5, acc0.astype(np.float64),
+                                dtype=oracle.DT_BF16)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(dev)  # noqa: E731
+    acc = torch.from_numpy(acc0).to(dev)
+    print(f"fused_score nh={nh} D={D}", flush=True)
+    wk.fused_score_accumulate(to_torch(q, "bfloat16", dev), to_torch(k, "bfloat16", dev), t(starts), t(ends),
+                              t(a_s), t(a_e), acc, t(offs))
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    ok, msg = allclose_report(acc.cpu().numpy().astype(np.float64), ref, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+def test_score_bad_audio_range_is_flagged():
+    """An audio range past its segment sets the device error word and is skipped."""
+    dev = torch.device("cuda", 0)
+    q = torch.zeros(2, 1, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(64, 128, dtype=torch.bfloat16, device=dev)
+    acc = torch.zeros(100, device=dev)
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)  # noqa: E731
+    wk.fused_score_accumulate(q, k, t([0, 10]), t([10, 20]), t([0, 0]), t([50, 5]), acc, t([0, 50, 55]))
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_BOUNDS
+    assert float(acc[:50].abs().sum()) == 0.0  # the bad item wrote nothing
+    assert _lib.device_error() == 0

@@ -251,3 +251,81 @@ def test_rebuild_max_evict_truncation():
     ok, _ = oracle.rebuild_append_kv(old, old, new, new, empty, empty, [0, 6], [0, 6], [-1], [0], [0, 2], [0, 3],
                                      [1, 4], 1)
     np.testing.assert_array_equal(ok[:, 0], [1, 2, 3, 4, 5, 9])
+
+
+# ---------------------------------------------------------------------------
+# class-A token scores (oracle_segment_scores)
+# ---------------------------------------------------------------------------
+def _np_scores(q, k, r0, r1, a0, a1, off, scale, acc_len):
+    """Independent formulation: numpy softmax per (item, head)."""
+    acc = np.zeros(acc_len)
+    for i in range(q.shape[0]):
+        seg = k[r0[i]:r1[i]].astype(np.float64)
+        logits = seg @ q[i].astype(np.float64).T * scale          # [rows, nh]
+        w = np.exp(logits - logits.max(axis=0))
+        w /= w.sum(axis=0)
+        acc[off[i]:off[i] + a1[i] - a0[i]] += w[a0[i]:a1[i]].sum(axis=1)
+    return acc
+
+
+def test_scores_whole_segment_sum_to_head_count():
+    """With the audio range = the whole segment, the weights of each head sum to 1."""
+    rng = np.random.default_rng(50)
+    nh, d = 3, 16
+    lens = [5, 40, 1]
+    k = rng.standard_normal((sum(lens), d)).astype(np.float32)
+    q = rng.standard_normal((3, nh, d)).astype(np.float32)
+    r0 = np.cumsum([0] + lens[:-1])
+    r1 = r0 + lens
+    acc = np.zeros(sum(lens))
+    oracle.segment_scores(q, k, r0, r1, [0] * 3, lens, r0, 0.3, acc, dtype=oracle.DT_F32)
+    for i in range(3):
+        assert abs(acc[r0[i]:r1[i]].sum() - nh) < 1e-12
+
+
+def test_scores_closed_forms():
+    d = 8
+    k = np.tile(np.arange(d, dtype=np.float32), (10, 1))  # equal keys: uniform weights
+    q = np.ones((1, 2, d), np.float32)
+    acc = np.zeros(4)
+    oracle.segment_scores(q, k, [0], [10], [3], [7], [0], 0.5, acc, dtype=oracle.DT_F32)
+    np.testing.assert_allclose(acc, [2 / 10] * 4, rtol=0, atol=1e-15)
+    acc = np.zeros(1)  # one row: weight exactly 1 per head
+    oracle.segment_scores(q, k[:1], [0], [1], [0], [1], [0], 0.5, acc, dtype=oracle.DT_F32)
+    assert acc[0] == 2.0
+
+
+def test_scores_match_numpy_and_accumulate():
+    rng = np.random.default_rng(51)
+    nh, d = 4, 32
+    lens = [30, 7, 64]
+    k = rng.standard_normal((120, d)).astype(np.float32)
+    q = rng.standard_normal((3, nh, d)).astype(np.float32)
+    r0 = np.array([2, 40, 50])  # arbitrary placement inside K (ranges may overlap)
+    r1 = r0 + lens
+    a0, a1 = np.array([3, 0, 10]), np.array([20, 7, 64])
+    off = np.array([0, 17, 24])
+    acc = np.full(24 + 54, 0.25)
+    want = _np_scores(q, k, r0, r1, a0, a1, off, 0.2, acc.size) + 0.25
+    oracle.segment_scores(q, k, r0, r1, a0, a1, off, 0.2, acc, dtype=oracle.DT_F32)
+    np.testing.assert_allclose(acc, want, rtol=1e-12, atol=1e-14)
+
+
+def test_attn_scores_maps_flagged_segments():
+    """Only segments of flagged KV heads contribute; audio offsets are per sample."""
+    rng = np.random.default_rng(52)
+    H, G, d = 3, 2, 16
+    lens = [12, 9, 15, 11, 8, 20]  # B = 2
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    k = rng.standard_normal((cu[-1], d)).astype(np.float32)
+    q = rng.standard_normal((6, G, d)).astype(np.float32)
+    mask = [0, 1, 1]
+    a_s, a_e, offs = [2, 1], [7, 6], [0, 5, 10]
+    acc = np.zeros(10)
+    oracle.attn_scores(q, k, cu, 0.25, mask, H, a_s, a_e, offs, acc, dtype=oracle.DT_F32)
+    want = np.zeros(10)
+    for s in range(6):
+        if mask[s % H]:
+            b = s // H
+            want += _np_scores(q[s:s + 1], k, [cu[s]], [cu[s + 1]], [a_s[b]], [a_e[b]], [offs[b]], 0.25, 10)
+    np.testing.assert_allclose(acc, want, rtol=1e-12, atol=1e-14)

@@ -50,6 +50,7 @@ struct AttnParams {
   float* part_acc;      // [slots, G, D]
   float* part_ml;       // [slots, G, 2]
   int32_t* counters;    // [n_seg]
+  float* lse;           // [n_seg, G, 2] final (max, sum) of each softmax, log2 domain, or null
   int32_t* err;
   int64_t kv_rows;
   int32_t n_seg;
@@ -145,6 +146,12 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
           T* o = (T*)p.out + (int64_t)i * p.G * D;
           const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
           for (int e = 0; e < p.G * D; ++e) Elem<T>::store(o, e, fill);
+          if (p.lse) {
+            for (int g = 0; g < p.G; ++g) {
+              p.lse[((int64_t)i * p.G + g) * 2] = len == 0 ? kNegBig : fill;
+              p.lse[((int64_t)i * p.G + g) * 2 + 1] = len == 0 ? 0.f : fill;
+            }
+          }
         }
         continue;
       }
@@ -240,7 +247,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // deterministic.  `lds` / `lds_bytes` is the workgroup's LDS, free here.
 template <typename T, int NT>
 __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, T* o,
-                                               uint8_t* lds, int lds_bytes) {
+                                               float* lse, uint8_t* lds, int lds_bytes) {
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -312,6 +319,10 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
     const int idx = tid + e * NT;
     if (idx < GD) Elem<T>::store(o, idx, accv[e] / gm[kMaxGroup + idx / D]);
   }
+  if (lse && tid < G) {
+    lse[tid * 2] = gm[tid];
+    lse[tid * 2 + 1] = gm[kMaxGroup + tid];
+  }
 }
 
 // Merge the NW wave states in LDS (layout: ml[w][g] = (m, l),
@@ -346,6 +357,10 @@ __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLd
         A += mrg_acc[(w * kMaxGroup + g) * D + (idx - g * D)] * sc;
       }
       Elem<T>::store(o, idx, A / L);
+      if (p.lse && idx - g * D == 0) {
+        p.lse[((int64_t)s * G + g) * 2] = M;
+        p.lse[((int64_t)s * G + g) * 2 + 1] = L;
+      }
     }
     __syncthreads();  // LDS reuse by the next piece
     return;
@@ -386,7 +401,7 @@ __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLd
   T* o = (T*)p.out + (int64_t)s * GD;
   const int np = (int)(p_last - p_first + 1);
   const int64_t s0 = p_first + s;  // slot of the first piece
-  combine_pieces<T, NT>(p, D, s0, np, o, lds, lds_bytes);
+  combine_pieces<T, NT>(p, D, s0, np, o, p.lse ? p.lse + (int64_t)s * G * 2 : nullptr, lds, lds_bytes);
   if (tid == 0) __hip_atomic_store(&p.counters[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
 }
@@ -877,11 +892,14 @@ extern "C" int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void
   return WNW_OK;
 }
 
-extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, const int32_t* cu_k,
-                                  const int64_t* seg_base, int64_t n_seg, int64_t group,
-                                  int64_t head_dim, int64_t total_rows, int64_t kv_rows, float scale,
-                                  int dtype, void* out, void* workspace, int64_t workspace_bytes,
-                                  int kernel, int64_t n_wg, void* stream) {
+namespace wnw {
+// Shared by the public attention entry points; lse (optional) receives each
+// segment's final softmax (max, sum) in the log2 domain, [n_seg, G, 2].
+int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                     const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
+                     int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
+                     void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
+                     void* stream) {
   WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1ll << 30), "n_seg out of range: %lld", (long long)n_seg);
   if (n_seg == 0) return WNW_OK;
   WNW_CHECK_ARG(q && cu_k && out && workspace && ((k && v) || kv_rows == 0), "null pointer argument");
@@ -922,6 +940,7 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
   ap.base = seg_base;
   ap.out = out;
   ap.counters = (int32_t*)((char*)workspace + L.counters);
+  ap.lse = lse;
   ap.part_ml = (float*)((char*)workspace + L.ml);
   ap.part_acc = (float*)((char*)workspace + L.acc);
   ap.err = device_error_word();
@@ -938,6 +957,17 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
   }
   WNW_CHECK_HIP(e, "decode attention launch");
   return WNW_OK;
+}
+
+}  // namespace wnw
+
+extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                                  const int64_t* seg_base, int64_t n_seg, int64_t group,
+                                  int64_t head_dim, int64_t total_rows, int64_t kv_rows, float scale,
+                                  int dtype, void* out, void* workspace, int64_t workspace_bytes,
+                                  int kernel, int64_t n_wg, void* stream) {
+  return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
+                          dtype, out, workspace, workspace_bytes, kernel, n_wg, nullptr, stream);
 }
 
 extern "C" int wnw_decode_attn(const void* q, const void* k, const void* v, const int32_t* cu_k,

@@ -28,8 +28,12 @@ class AttnWorkspace:
         self.buf: torch.Tensor | None = None
         self.counter_cap = 0  # n_seg whose counter region is known to be zero
 
-    def get(self, n_seg: int, group: int, head_dim: int) -> tuple[torch.Tensor, int]:
-        need = int(_lib.lib().wnw_decode_attn_workspace_bytes(n_seg, group, head_dim))
+    def get(self, n_seg: int, group: int, head_dim: int, score: bool = False) -> tuple[torch.Tensor, int]:
+        """Buffer and its size; ``score`` adds room for the softmax
+        normalisers of ``wnw_decode_attn_score``."""
+        query = _lib.lib().wnw_decode_attn_score_workspace_bytes if score else \
+            _lib.lib().wnw_decode_attn_workspace_bytes
+        need = int(query(n_seg, group, head_dim))
         if need < 0:
             raise _lib.WnwError("bad workspace query")
         if self.buf is None or self.buf.numel() < need:
@@ -127,3 +131,70 @@ def q1_decode_attn(
     """
     del block_n
     return decode_attn(q_flat, k_flat, v_flat, cu_k, scale)
+
+
+def q1_decode_attn_score(
+    q_flat: torch.Tensor,
+    k_flat: torch.Tensor,
+    v_flat: torch.Tensor,
+    cu_k: torch.Tensor,
+    scale: float,
+    ca_kv_mask: torch.Tensor,
+    num_kv_heads: int,
+    audio_starts: torch.Tensor,
+    audio_ends: torch.Tensor,
+    score_accumulator: torch.Tensor,
+    score_offsets: torch.Tensor,
+    block_n: int = 64,
+    *,
+    seg_base: torch.Tensor | None = None,
+    total_rows: int | None = None,
+    max_audio: int | None = None,
+    out: torch.Tensor | None = None,
+    workspace: AttnWorkspace | None = None,
+) -> torch.Tensor:
+    """Attention output [nseg, G, D] plus class-A score accumulation.
+
+    Reference: ``q1_decode_attn_score`` (src/common/kv/fused_attn.py:
+    126-156): for every segment whose KV head is flagged in ``ca_kv_mask``,
+    each audio token's softmax weight summed over the group's query heads is
+    added to ``score_accumulator[score_offsets[b] + token]``.  The weights
+    use the attention's own final softmax statistics.  ``max_audio`` (the
+    largest ``audio_ends - audio_starts``) sizes the scoring grid; when it is
+    not given it is read back from the device (one synchronisation).
+    """
+    del block_n
+    _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_accumulator,
+                     score_offsets, seg_base)
+    nseg, g, d = q_flat.shape
+    for name, t, n in (("ca_kv_mask", ca_kv_mask, num_kv_heads), ("audio_starts", audio_starts, nseg // num_kv_heads),
+                       ("audio_ends", audio_ends, nseg // num_kv_heads),
+                       ("score_offsets", score_offsets, nseg // num_kv_heads + 1)):
+        if t.dtype != torch.int32 or t.numel() != n:
+            raise _lib.WnwError(f"{name} must be int32 [{n}]")
+    if score_accumulator.dtype != torch.float32 or not score_accumulator.is_contiguous():
+        raise _lib.WnwError("score_accumulator must be a contiguous float32 tensor")
+    if k_flat.dim() != 2 or k_flat.shape[1] != d or v_flat.shape != k_flat.shape:
+        raise _lib.WnwError("k/v must be [rows, D] and equal")
+    if q_flat.dtype != k_flat.dtype or v_flat.dtype != k_flat.dtype:
+        raise _lib.WnwError("q, k and v must share a dtype")
+    if cu_k.dtype != torch.int32 or cu_k.numel() != nseg + 1:
+        raise _lib.WnwError("cu_k must be int32 [N+1]")
+    if max_audio is None:
+        max_audio = int((audio_ends - audio_starts).max().item()) if audio_ends.numel() else 0
+    q_flat, cu_k = q_flat.contiguous(), cu_k.contiguous()
+    ca_kv_mask, audio_starts, audio_ends, score_offsets = (
+        t.contiguous() for t in (ca_kv_mask, audio_starts, audio_ends, score_offsets))
+    if out is None:
+        out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
+    rows = k_flat.shape[0] if total_rows is None else int(total_rows)
+    _lib.ensure_init(q_flat.device)
+    ws = workspace if workspace is not None else workspace_for(q_flat.device)
+    buf, nbytes = ws.get(nseg, g, d, score=True)
+    _lib.check(_lib.lib().wnw_decode_attn_score(
+        _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base), nseg, g, d, rows,
+        k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(ca_kv_mask),
+        int(num_kv_heads), _lib.ptr(audio_starts), _lib.ptr(audio_ends), _lib.ptr(score_accumulator),
+        _lib.ptr(score_offsets), score_accumulator.numel(), int(max_audio), _lib.ptr(buf), nbytes,
+        _lib.stream_of(q_flat.device)), "q1_decode_attn_score")
+    return out

@@ -1,8 +1,9 @@
-"""Compaction kernels of the WnW cache.
+"""Compaction and scoring kernels of the WnW cache.
 
-Mirrors ``rebuild_append_kv`` of ``src/algorithms/wnw/code/kernels.py``:
-same arguments and result, computed by the gfx950 kernel
-``wnw_rebuild_append_kv`` of ``libwnw_amd.so``.
+Mirrors ``rebuild_append_kv`` and ``fused_score_accumulate`` of
+``src/algorithms/wnw/code/kernels.py``: same arguments and results, computed
+by the gfx950 kernels ``wnw_rebuild_append_kv`` and
+``wnw_fused_score_accumulate`` of ``libwnw_amd.so``.
 """
 from __future__ import annotations
 
@@ -68,3 +69,70 @@ def rebuild_append_kv(
         _lib.dtype_code(old_k.dtype), _lib.ptr(out_k), _lib.ptr(out_v), _lib.stream_of(old_k.device)),
         "rebuild_append_kv")
     return out_k, out_v
+
+
+_score_ws: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def fused_score_accumulate(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    seg_starts: torch.Tensor,
+    seg_ends: torch.Tensor,
+    audio_starts: torch.Tensor,
+    audio_ends: torch.Tensor,
+    accumulator: torch.Tensor,
+    accum_offsets: torch.Tensor,
+    *,
+    max_audio: int | None = None,
+    scale: float | None = None,
+) -> None:
+    """Full-segment softmax of each item's query heads, summed over the
+    heads, added to the accumulator at the audio rows.
+
+    Reference: ``fused_score_accumulate`` (src/algorithms/wnw/code/
+    kernels.py:302-348; ``_fused_score_pytorch`` :351-370 for any head
+    count).  Q: [S, nh, d]; K: [rows, d]; seg_starts/seg_ends [S] (rows of
+    K); audio_starts/audio_ends [S] relative to seg_starts; accumulator
+    float32, updated in place at ``accum_offsets[i] + j``.  ``scale``
+    defaults to d^-0.5 like the reference; ``max_audio`` (largest audio
+    range) is read back from the device when not given.
+    """
+    _lib.require_gpu(Q, K, seg_starts, seg_ends, audio_starts, audio_ends, accumulator, accum_offsets)
+    S, nh, d = Q.shape
+    for name, t, n in (("seg_starts", seg_starts, S), ("seg_ends", seg_ends, S), ("audio_starts", audio_starts, S),
+                       ("audio_ends", audio_ends, S), ("accum_offsets", accum_offsets, None)):
+        if t.dtype != torch.int32 or (n is not None and t.numel() != n):
+            raise _lib.WnwError(f"{name} must be int32 [{n if n is not None else 'S + 1'}]")
+    if accum_offsets.numel() < S + 1:
+        raise _lib.WnwError("accum_offsets must have at least S + 1 entries")
+    if accumulator.dtype != torch.float32 or not accumulator.is_contiguous():
+        raise _lib.WnwError("accumulator must be a contiguous float32 tensor")
+    if K.dim() != 2 or K.shape[1] != d or K.dtype != Q.dtype:
+        raise _lib.WnwError("K must be [rows, d] with the dtype of Q")
+    if K.shape[0] > 0 and (K.stride(1) != 1 or K.stride(0) != d):
+        raise _lib.WnwError("K rows must be contiguous")
+    if S == 0:
+        return
+    if max_audio is None:
+        max_audio = int((audio_ends - audio_starts).max().item())
+    if max_audio <= 0:
+        return
+    scale = d ** -0.5 if scale is None else float(scale)
+    Q = Q.contiguous()
+    seg_starts, seg_ends, audio_starts, audio_ends, accum_offsets = (
+        t.contiguous() for t in (seg_starts, seg_ends, audio_starts, audio_ends, accum_offsets))
+    need = int(_lib.lib().wnw_fused_score_workspace_bytes(S, nh))
+    dev = Q.device
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    ws = _score_ws.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=dev)
+        _score_ws[key] = ws
+    _lib.ensure_init(dev)
+    _lib.check(_lib.lib().wnw_fused_score_accumulate(
+        _lib.ptr(Q), _lib.ptr(K), _lib.ptr(seg_starts), _lib.ptr(seg_ends), _lib.ptr(audio_starts),
+        _lib.ptr(audio_ends), _lib.ptr(accumulator), _lib.ptr(accum_offsets), S, nh, d, K.shape[0],
+        accumulator.numel(), int(max_audio), scale, _lib.dtype_code(Q.dtype), _lib.ptr(ws), ws.numel(),
+        _lib.stream_of(dev)), "fused_score_accumulate")
