@@ -1,0 +1,166 @@
+"""End-to-end decode steps through WnWCache / WnWCppCache vs a CPU simulation.
+
+The cache is prefilled through its own hooks (random K/V and tie-free
+scores), then driven through ``decode_attention`` for several steps.  The
+simulation replays every step with the oracle: appends and compactions
+(bit-exact K/V, offsets), attention (2e-3 + 1e-2 |ref|), class-A scores
+(1e-6 + 1e-3 |ref|) and the planner's loaded segments.  The chunk top-k
+that the device computes from its own float32 scores is recorded and fed
+to the oracle planner, so both sides plan from the same chunks.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import planner as op
+from tests.helpers import allclose_report
+from wnw_amd import _lib
+from wnw_amd.wnw.cache import WnWCache
+from wnw_amd.wnw.config import WnWConfig
+from wnw_amd.wnw.session import decode_attention
+from wnw_amd.wnw_cpp.cache import WnWCppCache
+
+pytestmark = pytest.mark.gpu
+
+L, H, G, D, B = 2, 4, 4, 128, 2
+HQ = H * G
+S = 64
+AUDIO = [(8, 48), (4, 52)]
+STEPS = 8
+
+
+def _config():
+    return WnWConfig(chunk_size_s=8, overlap_s=4, token_rate=1.0,
+                     class_a=[0, 1, 2, 3, HQ + 4, HQ + 5],        # layer 0: whole group of KV 0; layer 1: half of KV 1
+                     class_b=[2, 3, H + 2, H + 3], retention_ratios=[0.5] * (L * H),
+                     top_k_chunks=2, eviction_lag=2, prefill_score_mode="last",
+                     num_layers=L, num_kv_heads=H, num_q_heads=HQ)
+
+
+def _recording(cls):
+    class Rec(cls):
+        def decode_all_layers_done(self):
+            self.rec_acc.append(self.score_accumulator.double().cpu().numpy().copy())
+            return super().decode_all_layers_done()
+
+        def _plan(self, topk, off):
+            o = off.tolist()
+            self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
+            return super()._plan(topk, off)
+    return Rec
+
+
+def _bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _prefill(cache, dev, gen):
+    starts = torch.tensor([a for a, _ in AUDIO], dtype=torch.int64, device=dev)
+    ends = torch.tensor([e for _, e in AUDIO], dtype=torch.int64, device=dev)
+    cache.setup_audio(starts, ends, None)
+    for l in range(L):
+        k = torch.randn(B, H, S, D, generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn(B, H, S, D, generator=gen, device=dev).to(torch.bfloat16)
+        ca = [torch.rand(e - a, generator=gen, device=dev) if cache.config.get_layer_class_a(l) else None
+              for a, e in AUDIO]
+        per = [[None if cache.config.is_class_a_kv_head(l, h) else torch.rand(e - a, generator=gen, device=dev)
+                for h in range(H)] for a, e in AUDIO]
+        cache.prefill_after_attn(l, ca, per, k, v)
+    cache.prefill_all_layers_done()
+
+
+@pytest.mark.parametrize("variant,fused", [("wnw", True), ("wnw", False), ("wnw_fallback", True),
+                                           ("wnw_cpp", True)])
+def test_decode_steps_match_simulation(variant, fused):
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    cls = _recording(WnWCppCache if variant == "wnw_cpp" else WnWCache)
+    cache = cls(_config(), L, H, HQ, D, dev)
+    cache.rec_acc, cache.rec_topk = [], []
+    if variant == "wnw_fallback":
+        cache.use_triton_rebuild = False
+    print(f"cache variant={variant} fused={fused}", flush=True)
+    _prefill(cache, dev, gen)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+
+    # simulation state, taken from the prefilled cache
+    K = [_bits(cache.layer_k[l]) for l in range(L)]
+    V = [_bits(cache.layer_v[l]) for l in range(L)]
+    lens = [list(cache.seq_lens[l]) for l in range(L)]
+    host_k, host_v = _bits(cache.cpu_restore_k), _bits(cache.cpu_restore_v)
+    meta = [[[[None if m is None else op.SegMeta(m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
+               for m in cache.restore_meta[l][b][h]] for h in range(H)] for b in range(B)] for l in range(L)]
+    o = op.PlannerOracle(L, H, B, 2, 2, cache.chunk_to_segs, [cache.config.get_layer_class_b(l) for l in range(L)],
+                         meta, copy.deepcopy(cache.loaded_segments), lens)
+    groups = []  # per layer: (kv, qheads)
+    for l in range(L):
+        by_kv = {}
+        for qh in cache.config.get_layer_class_a(l):
+            by_kv.setdefault(qh // G, []).append(qh)
+        groups.append(sorted(by_kv.items(), key=lambda x: x[0]))
+    audio_rel = [(a, e) for a, e in AUDIO]  # no left padding
+    offs = np.concatenate([[0], np.cumsum([e - a for a, e in AUDIO])])
+    scale = D ** -0.5
+    plan = None
+    n_plans = 0
+    for t in range(STEPS):
+        qs = [torch.randn(B, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+        ks = [torch.randn(B, H, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+        vs = [torch.randn(B, H, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
+        outs = [decode_attention(cache, l, qs[l], ks[l], vs[l], scale, fused=fused) for l in range(L)]
+        torch.cuda.synchronize()
+        assert _lib.device_error() == 0, f"step {t}"
+        # the plan made from the previous step's scores applies now
+        if t > 0:
+            o.seq_lens = [list(x) for x in lens]
+            plan = o.step(cache.rec_topk[t - 1])
+            n_plans += int(plan.any_change)
+        acc = np.zeros(int(offs[-1]))
+        for l in range(L):
+            nk = _bits(ks[l].reshape(B * H, D))
+            nv = _bits(vs[l].reshape(B * H, D))
+            cu_old = np.array(op.cu_from_lens(lens[l]), np.int32)
+            if plan is not None and plan.any_change:
+                load_k = np.concatenate([host_k[s:e] for s, e in plan.cpu_ranges]) if plan.cpu_ranges else \
+                    np.zeros((0, D), np.uint16)
+                load_v = np.concatenate([host_v[s:e] for s, e in plan.cpu_ranges]) if plan.cpu_ranges else \
+                    np.zeros((0, D), np.uint16)
+                cu_new = np.array(plan.cu_new[l], np.int32)
+                K[l], V[l] = oracle.rebuild_append_kv(
+                    K[l], V[l], nk, nv, load_k, load_v, cu_old, cu_new, plan.load_starts[l], plan.load_lens[l],
+                    plan.evict_offsets[l], plan.evict_starts[l], plan.evict_ends[l], plan.evict_max[l],
+                    dtype=oracle.DT_BF16)
+                lens[l] = list(plan.new_lens[l])
+            else:
+                cu_new = cu_old + np.arange(B * H + 1, dtype=np.int32)
+                K[l] = oracle.interleave_append(K[l], nk, cu_old, cu_new, dtype=oracle.DT_BF16)
+                V[l] = oracle.interleave_append(V[l], nv, cu_old, cu_new, dtype=oracle.DT_BF16)
+                lens[l] = [x + 1 for x in lens[l]]
+            np.testing.assert_array_equal(_bits(cache.layer_k[l]), K[l], err_msg=f"K step {t} layer {l}")
+            np.testing.assert_array_equal(_bits(cache.layer_v[l]), V[l], err_msg=f"V step {t} layer {l}")
+            cu = np.array(op.cu_from_lens(lens[l]), np.int32)
+            np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu)
+            q_flat = _bits(qs[l].reshape(B * H, G, D))
+            ref = oracle.decode_attn(q_flat, K[l], V[l], cu, scale, dtype=oracle.DT_BF16)
+            got = oracle.to_f64(_bits(outs[l].reshape(B * H, G, D)), oracle.DT_BF16)
+            ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+            assert ok, f"attention step {t} layer {l}: {msg}"
+            qfull = _bits(qs[l].reshape(B, HQ, D))
+            for kv, qheads in groups[l]:
+                segs = [b * H + kv for b in range(B)]
+                oracle.segment_scores(qfull[:, qheads], K[l], [cu[s] for s in segs], [cu[s + 1] for s in segs],
+                                      [a for a, _ in audio_rel], [e for _, e in audio_rel], offs[:-1], scale, acc,
+                                      dtype=oracle.DT_BF16)
+        ok, msg = allclose_report(cache.rec_acc[t], acc, 1e-6, 1e-3)
+        assert ok, f"scores step {t}: {msg}"
+    if variant != "wnw_cpp":  # the deferred variant plans at the next step's start
+        o.seq_lens = [list(x) for x in lens]
+        o.step(cache.rec_topk[STEPS - 1])
+    for b in range(B):
+        assert set(cache._planner.get_loaded_segments(b)) == o.loaded[b]
+    assert n_plans > 0, "no compaction happened: the test would be vacuous"

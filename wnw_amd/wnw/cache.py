@@ -1,0 +1,689 @@
+"""WnW KV cache on MI355X: flat varlen layout, class-A/B heads, chunk offload.
+
+Mirrors ``WnWCache`` (src/algorithms/wnw/code/cache.py:27-1010) hook for
+hook; every device operation is a kernel of ``libwnw_amd.so`` and every
+planning decision the native planner (``wnw_amd.wnw_cpp.planner``):
+
+decode step, per layer (cache.py:487-566)
+    ``decode_before_attn``      append (``interleave_append``), or the pending
+                                compaction + load + append
+                                (``rebuild_append_kv``) when a plan is active;
+    ``fused_decode_attention``  foldable class-A layer: attention + scores in
+                                one operator (``q1_decode_attn_score``), else
+                                attention then ``decode_after_attn``;
+    ``decode_after_attn``       class-A scores per KV group
+                                (``fused_score_accumulate``);
+after the last layer (cache.py:568-607)
+    ``decode_all_layers_done``  chunk means of the score accumulator ->
+                                top-k per sample -> native plan -> gather of
+                                the host rows into pinned staging -> H2D copy
+                                on a side stream with an event the next
+                                step's first rebuild waits for.
+
+Prefill (cache.py:236-390) builds the flat layout: class-A KV heads keep
+every token, other heads keep their per-segment top-k audio tokens plus all
+text; the pruned audio rows of class-B heads go to pinned host memory,
+grouped per (layer, sample, head, segment) (``restore_meta``), and the
+initial top-k chunks are loaded back.
+
+One deliberate difference: before the host refills the pinned staging
+buffer for a new plan it waits for the previous plan's H2D copy (the
+reference overwrites staging that an in-flight copy may still read).
+"""
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+from itertools import accumulate
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from ..kv.flat_cache import FlatVarlenCache
+from ..kv.fused_attn import q1_decode_attn, q1_decode_attn_score
+from ..kv.kernels import interleave_append
+from ..wnw_cpp.planner import Planner
+from .config import WnWConfig
+from .kernels import fused_score_accumulate, rebuild_append_kv
+
+
+@dataclass
+class SegmentMeta:
+    """cache.py:18-24: host rows of one offloaded segment and, when
+    resident, its rows relative to the start of its flat segment."""
+    cpu_start: int
+    cpu_end: int
+    gpu_rel_start: int = -1
+    gpu_rel_end: int = -1
+
+
+# ---------------------------------------------------------------------------
+# offsets and geometry (cache.py:1092-1111)
+# ---------------------------------------------------------------------------
+def _compute_segments(num_audio: int, stride: int) -> list[tuple[int, int]]:
+    return [(i * stride, min(i * stride + stride, num_audio)) for i in range(math.ceil(num_audio / stride))]
+
+
+def _compute_chunks(segments: list[tuple[int, int]], chunk_size: int, stride: int) -> list[list[int]]:
+    per = math.ceil(chunk_size / stride)
+    n = len(segments)
+    return [list(range(i, min(i + per, n))) for i in range(n)]
+
+
+def _build_cu_seqlens(seq_lens: list[int], device: torch.device) -> Tensor:
+    return torch.tensor(_build_cu_seqlens_list(seq_lens), dtype=torch.int32, device=device)
+
+
+def _build_cu_seqlens_list(seq_lens: list[int]) -> list[int]:
+    return [0] + list(accumulate(seq_lens))
+
+
+def _select_topk_per_segment(scores: Tensor, seg_ranges: list[tuple[int, int]], ratio: float) -> Tensor:
+    """cache.py:1114-1139: keep max(1, int(len * ratio)) top tokens per segment."""
+    kept = torch.zeros(scores.shape[0], dtype=torch.bool, device=scores.device)
+    for s, e in seg_ranges:
+        if e > s:
+            kept[scores[s:e].topk(max(1, int((e - s) * ratio))).indices + s] = True
+    return kept
+
+
+def _select_topk_global(scores: Tensor, seg_ranges: list[tuple[int, int]], ratio: float) -> Tensor:
+    """cache.py:1142-1150: the same budget, chosen over the whole audio range."""
+    n_keep = min(sum(max(1, int((e - s) * ratio)) for s, e in seg_ranges), scores.shape[0])
+    kept = torch.zeros(scores.shape[0], dtype=torch.bool, device=scores.device)
+    kept[scores.topk(n_keep).indices] = True
+    return kept
+
+
+def _invert_ranges(ranges: list[tuple[int, int]], total_len: int) -> list[tuple[int, int]]:
+    """cache.py:1153-1162: complement of sorted disjoint ranges in [0, total_len)."""
+    out, prev = [], 0
+    for s, e in ranges:
+        if prev < s:
+            out.append((prev, s))
+        prev = e
+    if prev < total_len:
+        out.append((prev, total_len))
+    return out
+
+
+class WnWCache(FlatVarlenCache):
+    """WnW KV cache manager (see the module docstring for the step flow)."""
+
+    def __init__(self, config: WnWConfig, num_layers: int, num_kv_heads: int, num_q_heads: int, head_dim: int,
+                 device: torch.device, adapter=None):
+        super().__init__(num_layers, num_kv_heads, num_q_heads, head_dim, device, adapter)
+        if config.num_layers == 0:
+            config.set_model_dims(num_layers, num_kv_heads, num_q_heads)
+        self.config = config
+        self.batch_size = 0
+        self.layer_k: list[Tensor | None] = [None] * num_layers
+        self.layer_v: list[Tensor | None] = [None] * num_layers
+        self.cu_seqlens_k: list[Tensor | None] = [None] * num_layers
+        self.cu_seqlens_list: list[list[int] | None] = [None] * num_layers
+        self.seq_lens: list[list[int] | None] = [None] * num_layers
+        self.cpu_restore_k: Tensor | None = None
+        self.cpu_restore_v: Tensor | None = None
+        self.restore_meta: list = []
+        self.loaded_segments: list[set[int]] = []
+        self.score_accumulator: Tensor | None = None
+        self.score_offsets: Tensor | None = None
+        # a5: the out-of-place compaction fallback (cache.py:891-1010)
+        self.use_triton_rebuild = os.environ.get("WNW_DISABLE_TRITON_REBUILD", "0") != "1"
+        self._class_b_heads_by_layer = [config.get_layer_class_b(l) for l in range(num_layers)]
+        self._transfer_stream: torch.cuda.Stream | None = None
+        self._planner: Planner | None = None
+        self._staging_k: Tensor | None = None
+        self._staging_v: Tensor | None = None
+        self._decode_step = 0
+        self._clear_pending_rebuild_state()
+
+    # ------------------------------------------------------------------ setup
+    def setup_audio(self, audio_starts: Tensor, audio_ends: Tensor, attention_mask: Tensor | None = None) -> None:
+        """cache.py:144-166."""
+        super().setup_audio(audio_starts, audio_ends, attention_mask)
+        starts, ends, pads = audio_starts.tolist(), audio_ends.tolist(), self.pad_lens.tolist()
+        self.batch_size = len(starts)
+        self._setup_segments(starts, ends, pads)
+        self._setup_score_buffers(starts, ends, pads)
+        self._setup_chunk_state()
+
+    def _setup_segments(self, starts, ends, pads) -> None:
+        """cache.py:168-210: segments, chunks and chunk token bounds per sample."""
+        self._raw_audio_starts, self._raw_audio_ends = list(starts), list(ends)
+        self.pad_lens_list = list(pads)
+        self._audio_starts_list = [s - p for s, p in zip(starts, pads)]
+        self._audio_ends_list = [e - p for e, p in zip(ends, pads)]
+        stride, chunk = self.config.stride_tokens, self.config.chunk_size_tokens
+        self.segment_ranges = [_compute_segments(e - s, stride)
+                               for s, e in zip(self._audio_starts_list, self._audio_ends_list)]
+        self.chunk_to_segs = [_compute_chunks(r, chunk, stride) for r in self.segment_ranges]
+        self._chunk_token_bounds = [
+            [(r[c[0]][0], r[c[-1]][1]) if c else (0, 0) for c in c2s]
+            for r, c2s in zip(self.segment_ranges, self.chunk_to_segs)
+        ]
+
+    def _setup_score_buffers(self, starts, ends, pads) -> None:
+        """cache.py:212-221: one float32 accumulator over every sample's audio."""
+        self._prefill_scores = [[] for _ in range(self.batch_size)]
+        lens = [e - s for s, e in zip(starts, ends)]
+        self._score_offsets_list = [0] + list(accumulate(lens))
+        self.score_offsets = torch.tensor(self._score_offsets_list, dtype=torch.int32, device=self.device)
+        self.score_accumulator = torch.zeros(self._score_offsets_list[-1], dtype=torch.float32, device=self.device)
+        self._max_audio = max(lens) if lens else 0
+
+    def _setup_chunk_state(self) -> None:
+        """cache.py:223-248."""
+        L, B, H = self.num_layers, self.batch_size, self.num_kv_heads
+        self.loaded_segments = [set() for _ in range(B)]
+        self.layer_k = [None] * L
+        self.layer_v = [None] * L
+        self.cu_seqlens_k = [None] * L
+        self.cu_seqlens_list = [None] * L
+        self.seq_lens = [None] * L
+        self.restore_meta = [[[[None] * len(self.segment_ranges[b]) for _ in range(H)] for b in range(B)]
+                             for _ in range(L)]
+        self._cpu_buffers_k, self._cpu_buffers_v, self._cpu_buffer_metas = [], [], []
+        self._pending_chunk_update = False
+        self._decode_step = 0
+        self._planner = None
+        self._clear_pending_rebuild_state()
+
+    def _clear_pending_rebuild_state(self) -> None:
+        L = self.num_layers
+        self._pending_transfer_event: torch.cuda.Event | None = None
+        self._pending_transfer_waited = False
+        self._pending_gpu_k: Tensor | None = None
+        self._pending_gpu_v: Tensor | None = None
+        self._pending_load_starts: list = [None] * L
+        self._pending_load_lens: list = [None] * L
+        self._pending_evict_offsets: list = [None] * L
+        self._pending_evict_starts: list = [None] * L
+        self._pending_evict_ends: list = [None] * L
+        self._pending_evict_max = [0] * L
+        self._pending_new_lens: list = [None] * L
+        self._pending_cu_new: list = [None] * L
+        self._pending_layers_applied = 0
+
+    def _get_transfer_stream(self) -> torch.cuda.Stream:
+        if self._transfer_stream is None:
+            self._transfer_stream = torch.cuda.Stream(device=self.device)  # default priority
+        return self._transfer_stream
+
+    # ---------------------------------------------------------------- prefill
+    def prefill_before_attn(self, layer_idx: int) -> None:
+        self.stats.record_prefill_before(self._snapshot_cache_stats)
+
+    def prefill_after_attn(self, layer_idx: int, class_a_scores: list, per_head_scores: list, key_states: Tensor,
+                           value_states: Tensor) -> None:
+        """cache.py:254-337: build this layer's flat K/V; offload the pruned
+        audio rows of class-B heads to the host, grouped per segment."""
+        for b in range(self.batch_size):
+            if class_a_scores[b] is not None:
+                self._prefill_scores[b].append(class_a_scores[b])
+        pieces_k, pieces_v, lens = [], [], []
+        stride = self.config.stride_tokens
+        for b in range(self.batch_size):
+            ra, re, pad = self._raw_audio_starts[b], self._raw_audio_ends[b], self.pad_lens_list[b]
+            for h in range(self.num_kv_heads):
+                k_full, v_full = key_states[b, h], value_states[b, h]
+                if self.config.is_class_a_kv_head(layer_idx, h):
+                    pieces_k.append(k_full[pad:])
+                    pieces_v.append(v_full[pad:])
+                    lens.append(k_full.shape[0] - pad)
+                    continue
+                ratio = self.config.get_retention(layer_idx, h)
+                select = _select_topk_global if self.config.prefill_global_topk else _select_topk_per_segment
+                kept = select(per_head_scores[b][h], self.segment_ranges[b], ratio)
+                text_k = torch.cat([k_full[pad:ra], k_full[re:]])
+                text_v = torch.cat([v_full[pad:ra], v_full[re:]])
+                audio_k, audio_v = k_full[ra:re], v_full[ra:re]
+                pieces_k.append(torch.cat([text_k, audio_k[kept]]))
+                pieces_v.append(torch.cat([text_v, audio_v[kept]]))
+                lens.append(text_k.shape[0] + int(kept.sum().item()))
+                if self.config.is_class_b(layer_idx, h):
+                    idx = (~kept).nonzero(as_tuple=True)[0]
+                    if idx.numel() == 0:
+                        continue
+                    rk, rv = audio_k.index_select(0, idx).cpu(), audio_v.index_select(0, idx).cpu()
+                    self.stats.record_cpu_gpu_transfer(b, g2c_tokens=int(idx.numel()),
+                                                       g2c_bytes=int((rk.numel() + rv.numel()) * rk.element_size()))
+                    counts = torch.bincount(idx // stride, minlength=len(self.segment_ranges[b])).tolist()
+                    o = 0
+                    for si, n in enumerate(counts):
+                        if n > 0:
+                            self._cpu_buffers_k.append(rk[o:o + n])
+                            self._cpu_buffers_v.append(rv[o:o + n])
+                            self._cpu_buffer_metas.append((layer_idx, b, h, si, n))
+                            o += n
+        self.layer_k[layer_idx] = torch.cat(pieces_k)
+        self.layer_v[layer_idx] = torch.cat(pieces_v)
+        self.seq_lens[layer_idx] = lens
+        self.cu_seqlens_k[layer_idx] = _build_cu_seqlens(lens, self.device)
+        self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(lens)
+
+    def prefill_all_layers_done(self) -> None:
+        """cache.py:339-390: pin the host rows, index them, load the initial
+        top-k chunks, hand the state to the native planner."""
+        if self._cpu_buffers_k:
+            self.cpu_restore_k = torch.cat(self._cpu_buffers_k).pin_memory()
+            self.cpu_restore_v = torch.cat(self._cpu_buffers_v).pin_memory()
+            o = 0
+            for l, b, h, si, n in self._cpu_buffer_metas:
+                self.restore_meta[l][b][h][si] = SegmentMeta(o, o + n)
+                o += n
+        else:
+            dt = self.layer_k[0].dtype if self.layer_k[0] is not None else torch.bfloat16
+            self.cpu_restore_k = torch.empty(0, self.head_dim, dtype=dt)
+            self.cpu_restore_v = torch.empty(0, self.head_dim, dtype=dt)
+        self._cpu_buffers_k, self._cpu_buffers_v, self._cpu_buffer_metas = [], [], []
+        for b in range(self.batch_size):
+            if self._prefill_scores[b]:
+                avg = torch.stack(self._prefill_scores[b]).sum(dim=0)
+            else:
+                avg = torch.ones(self._audio_ends_list[b] - self._audio_starts_list[b], device=self.device)
+            self._select_and_apply_chunks(b, avg)
+            self._prefill_scores[b].clear()
+        self.prefilled = True
+        self._init_planner()
+        self._precompute_decode_constants()
+        self.stats.record_prefill(self._snapshot_cache_stats)
+
+    def load_prefilled_state(self, layer_k: list[Tensor], layer_v: list[Tensor], seq_lens: list[list[int]],
+                             cpu_restore_k: Tensor, cpu_restore_v: Tensor, restore_meta: list,
+                             loaded_segments: list[set[int]]) -> None:
+        """Install the state ``prefill_all_layers_done`` leaves (flat layers,
+        pinned host rows, ``restore_meta`` [L][B][H][seg] of SegmentMeta or
+        None, loaded segments) without running a model prefill; call after
+        ``setup_audio``."""
+        for l in range(self.num_layers):
+            self.layer_k[l], self.layer_v[l] = layer_k[l], layer_v[l]
+            self.seq_lens[l] = list(seq_lens[l])
+            self.cu_seqlens_k[l] = _build_cu_seqlens(self.seq_lens[l], self.device)
+            self.cu_seqlens_list[l] = _build_cu_seqlens_list(self.seq_lens[l])
+        self.cpu_restore_k = cpu_restore_k if cpu_restore_k.is_pinned() else cpu_restore_k.pin_memory()
+        self.cpu_restore_v = cpu_restore_v if cpu_restore_v.is_pinned() else cpu_restore_v.pin_memory()
+        self.restore_meta = restore_meta
+        self.loaded_segments = [set(s) for s in loaded_segments]
+        self.prefilled = True
+        self._init_planner()
+        self._precompute_decode_constants()
+
+    def _select_and_apply_chunks(self, b: int, scores: Tensor) -> None:
+        """cache.py:603-607: initial chunk choice of a sample, loaded at once."""
+        to_load = self._initial_chunk_changes(b, self._topk_of(b, scores))
+        if to_load:
+            self._load_segments_for_sample(b, to_load)
+        self.loaded_segments[b] = to_load
+
+    def _initial_chunk_changes(self, b: int, topk_chunks: list[int]) -> set[int]:
+        """cache.py:609-630 at prefill time: nothing is loaded yet, so the
+        chunks' segments are loaded and nothing is evicted (the decode-time
+        rule with eviction lag is the native planner's)."""
+        return {si for c in topk_chunks for si in self.chunk_to_segs[b][c]} - self.loaded_segments[b]
+
+    def _topk_of(self, b: int, scores: Tensor) -> list[int]:
+        """cache.py:632-649: mean score per chunk (prefix sums), top-k."""
+        bounds = self._chunk_token_bounds[b]
+        k = min(self.config.top_k_chunks, len(bounds))
+        if k == 0:
+            return []
+        prefix = torch.zeros(scores.shape[0] + 1, dtype=torch.float32, device=scores.device)
+        torch.cumsum(scores.float(), dim=0, out=prefix[1:])
+        st = torch.tensor([s for s, _ in bounds], dtype=torch.int64, device=scores.device)
+        en = torch.tensor([e for _, e in bounds], dtype=torch.int64, device=scores.device)
+        means = (prefix[en] - prefix[st]) / (en - st).clamp(min=1).float()
+        return means.topk(k).indices.tolist()
+
+    def _load_segments_for_sample(self, b: int, segs: set[int]) -> None:
+        """cache.py:651-714: append the host rows of `segs` to every class-B
+        segment of sample b, in segment order (prefill only)."""
+        order = sorted(segs)
+        for l in range(self.num_layers):
+            cu = self.cu_seqlens_list[l]
+            pieces_k, pieces_v, lens = [], [], []
+            for f in range(self.batch_size * self.num_kv_heads):
+                fb, h = divmod(f, self.num_kv_heads)
+                s, e = cu[f], cu[f + 1]
+                pieces_k.append(self.layer_k[l][s:e])
+                pieces_v.append(self.layer_v[l][s:e])
+                cursor, extra = e - s, 0
+                if fb == b and self.config.is_class_b(l, h):
+                    for si in order:
+                        m = self.restore_meta[l][fb][h][si]
+                        if m is None:
+                            continue
+                        n = m.cpu_end - m.cpu_start
+                        pieces_k.append(self.cpu_restore_k[m.cpu_start:m.cpu_end].to(self.device))
+                        pieces_v.append(self.cpu_restore_v[m.cpu_start:m.cpu_end].to(self.device))
+                        m.gpu_rel_start, m.gpu_rel_end = cursor, cursor + n
+                        cursor += n
+                        extra += n
+                        self.stats.record_cpu_gpu_transfer(b, c2g_tokens=n, c2g_bytes=2 * n * self.head_dim *
+                                                           self.cpu_restore_k.element_size())
+                lens.append(e - s + extra)
+            self.layer_k[l] = torch.cat(pieces_k)
+            self.layer_v[l] = torch.cat(pieces_v)
+            self.seq_lens[l] = lens
+            self.cu_seqlens_k[l] = _build_cu_seqlens(lens, self.device)
+            self.cu_seqlens_list[l] = _build_cu_seqlens_list(lens)
+
+    def _init_planner(self) -> None:
+        """Hand segments, chunks, class-B heads, restore metadata, loaded sets
+        and lengths to the native planner (src/algorithms/wnw_cpp/code/
+        cache.py:40-120 does the same for the reference's C++ planner)."""
+        L, H, B = self.num_layers, self.num_kv_heads, self.batch_size
+        p = Planner(L, H, B, self.num_kv_groups)
+        p.set_config(self.config.top_k_chunks, self.config.eviction_lag)
+        p.set_seg_count([len(self.segment_ranges[b]) for b in range(B)])
+        for b in range(B):
+            flat, off = [], [0]
+            for segs in self.chunk_to_segs[b]:
+                flat += segs
+                off.append(len(flat))
+            p.set_chunk_to_segs(b, flat, off)
+        for l in range(L):
+            p.set_class_b(l, self._class_b_heads_by_layer[l])
+        cs, ce, gs, ge = [], [], [], []
+        for l in range(L):
+            for f in range(B * H):
+                b, h = divmod(f, H)
+                for m in self.restore_meta[l][b][h]:
+                    if m is None:
+                        cs.append(-1), ce.append(-1), gs.append(-1), ge.append(-1)
+                    else:
+                        cs.append(m.cpu_start), ce.append(m.cpu_end)
+                        gs.append(m.gpu_rel_start), ge.append(m.gpu_rel_end)
+        p.set_restore_meta(cs, ce, gs, ge)
+        for b in range(B):
+            p.set_loaded(b, sorted(self.loaded_segments[b]))
+        p.set_seq_lens([x for l in range(L) for x in self.seq_lens[l]])
+        n_restore = self.cpu_restore_k.shape[0]
+        if n_restore > 0:
+            self._staging_k = torch.empty(n_restore, self.head_dim, dtype=self.cpu_restore_k.dtype, pin_memory=True)
+            self._staging_v = torch.empty(n_restore, self.head_dim, dtype=self.cpu_restore_v.dtype, pin_memory=True)
+            p.set_restore_buffers(self.cpu_restore_k, self.cpu_restore_v, self._staging_k, self._staging_v)
+        N = B * H
+        self._plan_out = dict(
+            load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
+            cu_new_2d=torch.empty(L, N + 1, dtype=torch.int32), new_lens_2d=torch.empty(L, N, dtype=torch.int32),
+            evict_offsets_2d=torch.empty(L, N + 1, dtype=torch.int32), evict_max=torch.empty(L, dtype=torch.int32),
+            evict_layer_ptr=torch.empty(L + 1, dtype=torch.int32))
+        self._planner = p
+
+    def _precompute_decode_constants(self) -> None:
+        """cache.py:392-484: per-layer class-A groups by KV head, foldable
+        layers (whole GQA groups class A) and their KV masks, audio ranges."""
+        N = self.batch_size * self.num_kv_heads
+        _lib.ensure_init(self.device)  # module load and device error word (replaces the Triton warm-up)
+        self._cu_step_increment = torch.arange(N + 1, dtype=torch.int32, device=self.device)
+        self._empty_i32 = torch.empty(0, dtype=torch.int32, device=self.device)
+        G = self.num_kv_groups
+        self._decode_after_groups = [[] for _ in range(self.num_layers)]
+        self._layer_foldable, self._ca_kv_mask_by_layer = [], []
+        self._decode_class_a_local = None
+        for l in range(self.num_layers):
+            ca = self.config.get_layer_class_a(l)
+            if ca and self._decode_class_a_local is None:
+                self._decode_class_a_local = ca
+            by_kv: dict[int, list[int]] = {}
+            for qh in ca:
+                by_kv.setdefault(qh // G, []).append(qh)
+            for kv, qheads in sorted(by_kv.items()):
+                seg_idx = torch.tensor([b * self.num_kv_heads + kv for b in range(self.batch_size)],
+                                       dtype=torch.int64, device=self.device)
+                self._decode_after_groups[l].append((qheads, seg_idx))
+            foldable = bool(ca) and all(set(range(kv * G, (kv + 1) * G)) <= set(ca) for kv in by_kv)
+            self._layer_foldable.append(foldable)
+            if foldable:
+                mask = torch.zeros(self.num_kv_heads, dtype=torch.int32)
+                mask[list(by_kv)] = 1
+                self._ca_kv_mask_by_layer.append(mask.to(self.device))
+            else:
+                self._ca_kv_mask_by_layer.append(None)
+        self._decode_audio_starts_b = torch.tensor(self._audio_starts_list, dtype=torch.int32, device=self.device)
+        self._decode_audio_ends_b = torch.tensor(self._audio_ends_list, dtype=torch.int32, device=self.device)
+        # chunk scoring on the device: padded [B, W] prefix sums of the accumulator
+        B = self.batch_size
+        W = self._max_audio + 1
+        scatter, gk_s, gk_e, gk_len, gk_pos = [], [], [], [], []
+        self._max_chunks = max((len(c) for c in self.chunk_to_segs), default=0)
+        for b in range(B):
+            base = b * W
+            n = self._score_offsets_list[b + 1] - self._score_offsets_list[b]
+            scatter += range(base + 1, base + 1 + n)
+            for c, (s, e) in enumerate(self._chunk_token_bounds[b]):
+                gk_s.append(base + s)
+                gk_e.append(base + e)
+                gk_len.append(max(1, e - s))
+                gk_pos.append(b * self._max_chunks + c)
+        dev = self.device
+        self._tk_scatter = torch.tensor(scatter, dtype=torch.int64, device=dev)
+        self._tk_s = torch.tensor(gk_s, dtype=torch.int64, device=dev)
+        self._tk_e = torch.tensor(gk_e, dtype=torch.int64, device=dev)
+        self._tk_len = torch.tensor(gk_len, dtype=torch.float32, device=dev)
+        self._tk_pos = torch.tensor(gk_pos, dtype=torch.int64, device=dev)
+        self._tk_padded = torch.zeros(B, W, dtype=torch.float32, device=dev)
+        self._tk_prefix = torch.empty(B, W, dtype=torch.float32, device=dev)
+        self._tk_grid = torch.full((B * max(1, self._max_chunks),), float("-inf"), dtype=torch.float32, device=dev)
+        self._tk_k = min(self.config.top_k_chunks, self._max_chunks)
+
+    # ----------------------------------------------------------------- decode
+    def decode_before_attn(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
+        """cache.py:487-515: returns (K, V, cu_seqlens_k, max_seqlen_k)."""
+        if self._pending_chunk_update:
+            if self.use_triton_rebuild and self._pending_cu_new[layer_idx] is not None:
+                return self._rebuild_append_layer(layer_idx, new_k, new_v)
+            self._apply_chunk_update_to_layer(layer_idx)
+        nk = new_k.squeeze(2).reshape(-1, self.head_dim)
+        nv = new_v.squeeze(2).reshape(-1, self.head_dim)
+        cu_old = self.cu_seqlens_k[layer_idx]
+        new_lens = [x + 1 for x in self.seq_lens[layer_idx]]
+        cu_new = cu_old + self._cu_step_increment
+        k = interleave_append(self.layer_k[layer_idx], nk, cu_old, cu_new)
+        v = interleave_append(self.layer_v[layer_idx], nv, cu_old, cu_new)
+        self.layer_k[layer_idx], self.layer_v[layer_idx] = k, v
+        self.seq_lens[layer_idx] = new_lens
+        self.cu_seqlens_k[layer_idx] = cu_new
+        self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(new_lens)
+        return k, v, cu_new, max(new_lens)
+
+    def decode_after_attn(self, layer_idx: int, q: Tensor) -> None:
+        """cache.py:517-544: class-A scores, each KV group against its own
+        segment (softmax over the whole segment, summed over its heads)."""
+        if self._decode_class_a_local is None or not self._decode_after_groups[layer_idx]:
+            return
+        cu = self.cu_seqlens_k[layer_idx]
+        K = self.layer_k[layer_idx]
+        for qheads, seg_idx in self._decode_after_groups[layer_idx]:
+            Q = q[:, qheads, 0, :]
+            fused_score_accumulate(Q, K, cu[seg_idx].to(torch.int32), cu[seg_idx + 1].to(torch.int32),
+                                   self._decode_audio_starts_b, self._decode_audio_ends_b, self.score_accumulator,
+                                   self.score_offsets, max_audio=self._max_audio)
+
+    def fused_decode_attention(self, layer_idx, q_flat, q, k_flat, v_flat, cu_k, scale):
+        """cache.py:546-566: foldable class-A layers score inside the
+        attention operator; other class-A layers score afterwards."""
+        if self._layer_foldable[layer_idx]:
+            return q1_decode_attn_score(q_flat, k_flat, v_flat, cu_k, scale, self._ca_kv_mask_by_layer[layer_idx],
+                                        self.num_kv_heads, self._decode_audio_starts_b, self._decode_audio_ends_b,
+                                        self.score_accumulator, self.score_offsets, max_audio=self._max_audio)
+        out = q1_decode_attn(q_flat, k_flat, v_flat, cu_k, scale)
+        self.decode_after_attn(layer_idx, q)
+        return out
+
+    def decode_all_layers_done(self) -> None:
+        """cache.py:568-576."""
+        self._decode_step += 1
+        self.stats.flush_decode_step(self._decode_step)
+        if self.stats.enabled and self._decode_step % self.stats.interval == 0:
+            self.stats.record_decode(self._decode_step, self._snapshot_cache_stats)
+        any_change = self._compute_decode_chunk_update()
+        self._prepare_decode_rebuild_if_needed(any_change)
+        self.score_accumulator.zero_()
+
+    # ---------------------------------------------------------------- planning
+    def _topk_scores_async(self) -> Tensor | None:
+        """Top-k chunks of every sample from the accumulator, on the device
+        (src/algorithms/wnw_cpp/code/cache.py:160-171): chunk means from
+        padded prefix sums, -1 where a sample has fewer chunks than k."""
+        if self._tk_k == 0:
+            return None
+        self._tk_padded.view(-1).index_copy_(0, self._tk_scatter, self.score_accumulator)
+        torch.cumsum(self._tk_padded, dim=1, out=self._tk_prefix)
+        pf = self._tk_prefix.view(-1)
+        self._tk_grid.index_copy_(0, self._tk_pos, (pf[self._tk_e] - pf[self._tk_s]) / self._tk_len)
+        vals, idx = self._tk_grid.view(self.batch_size, self._max_chunks).topk(self._tk_k, dim=1)
+        idx = idx.to(torch.int32)
+        return torch.where(vals > float("-inf"), idx, torch.full_like(idx, -1))
+
+    def _topk_finalize(self, idx_masked: Tensor | None) -> tuple[Tensor, Tensor]:
+        """CSR of the chosen chunks per sample (wnw_cpp/code/cache.py:173-189)."""
+        if idx_masked is None:
+            return torch.empty(0, dtype=torch.int32), torch.zeros(self.batch_size + 1, dtype=torch.int32)
+        flat, off = [], [0]
+        for row in idx_masked.tolist():
+            flat += [c for c in row if c >= 0]
+            off.append(len(flat))
+        return torch.tensor(flat, dtype=torch.int32), torch.tensor(off, dtype=torch.int32)
+
+    def _compute_decode_chunk_update(self) -> bool:
+        """cache.py:578-593 + the chunk changes (:609-649): top-k per sample
+        from this step's scores, then the native plan of every layer."""
+        self._pending_chunk_update = False
+        topk, off = self._topk_finalize(self._topk_scores_async())
+        return self._plan(topk, off)
+
+    def _plan(self, topk: Tensor, off: Tensor) -> bool:
+        flag, total, ev_s, ev_e, ranges = self._planner.compute_and_prepare(topk, off, **self._plan_out)
+        self._plan_result = (total, ev_s, ev_e, ranges)
+        return bool(flag)
+
+    def _prepare_decode_rebuild_if_needed(self, any_change: bool, activate: bool = True) -> None:
+        """cache.py:595-600."""
+        if any_change:
+            if activate:
+                self._pending_chunk_update = True
+            self._prepare_pending_rebuild()
+
+    def _prepare_pending_rebuild(self) -> None:
+        """cache.py:756-889 with the native plan: per-layer descriptors on the
+        device, host rows gathered into pinned staging and copied on the
+        transfer stream."""
+        total, ev_s, ev_e, ranges = self._plan_result
+        prev_event = self._pending_transfer_event
+        self._clear_pending_rebuild_state()
+        o = self._plan_out
+        dev = self.device
+        ls, ll, cun = (o["load_starts_2d"].to(dev), o["load_lens_2d"].to(dev), o["cu_new_2d"].to(dev))
+        eoff = o["evict_offsets_2d"].to(dev)
+        evs = ev_s.to(dev) if ev_s.numel() else self._empty_i32
+        eve = ev_e.to(dev) if ev_e.numel() else self._empty_i32
+        elp, emax, new_lens = o["evict_layer_ptr"].tolist(), o["evict_max"].tolist(), o["new_lens_2d"].tolist()
+        for l in range(self.num_layers):
+            self._pending_load_starts[l], self._pending_load_lens[l], self._pending_cu_new[l] = ls[l], ll[l], cun[l]
+            self._pending_evict_offsets[l] = eoff[l]
+            self._pending_evict_max[l] = emax[l]
+            self._pending_new_lens[l] = new_lens[l]
+            lo, hi = elp[l], elp[l + 1]
+            self._pending_evict_starts[l] = evs[lo:hi] if hi > lo else self._empty_i32
+            self._pending_evict_ends[l] = eve[lo:hi] if hi > lo else self._empty_i32
+        self._segments_changed_ranges = ranges
+        dt = self.layer_k[0].dtype
+        if total > 0:
+            if prev_event is not None:
+                prev_event.synchronize()  # the previous copy has left staging
+            self._planner.gather_restore()
+            stream = self._get_transfer_stream()
+            ev = torch.cuda.Event()
+            with torch.cuda.stream(stream):
+                self._pending_gpu_k = self._staging_k[:total].to(dev, non_blocking=True)
+                self._pending_gpu_v = self._staging_v[:total].to(dev, non_blocking=True)
+                ev.record(stream)
+            self._pending_transfer_event = ev
+        else:
+            self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
+            self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
+
+    def _rebuild_append_layer(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
+        """cache.py:716-754: compaction + load + append in one launch."""
+        if self._pending_transfer_event is not None and not self._pending_transfer_waited:
+            torch.cuda.current_stream(self.device).wait_event(self._pending_transfer_event)
+            self._pending_transfer_waited = True
+        nk = new_k.squeeze(2).reshape(-1, self.head_dim)
+        nv = new_v.squeeze(2).reshape(-1, self.head_dim)
+        cu_new = self._pending_cu_new[layer_idx]
+        new_lens = self._pending_new_lens[layer_idx]
+        k, v = rebuild_append_kv(
+            self.layer_k[layer_idx], self.layer_v[layer_idx], nk, nv, self._pending_gpu_k, self._pending_gpu_v,
+            self.cu_seqlens_k[layer_idx], cu_new, self._pending_load_starts[layer_idx],
+            self._pending_load_lens[layer_idx], self._pending_evict_offsets[layer_idx],
+            self._pending_evict_starts[layer_idx], self._pending_evict_ends[layer_idx],
+            self._pending_evict_max[layer_idx], total_out=sum(new_lens))
+        self._finish_layer(layer_idx, k, v, cu_new, new_lens)
+        return k, v, cu_new, max(new_lens)
+
+    def _apply_chunk_update_to_layer(self, layer_idx: int) -> None:
+        """cache.py:891-1010 (the fallback without the fused append): the
+        same compaction and load, then the ordinary append follows."""
+        if self._pending_transfer_event is not None and not self._pending_transfer_waited:
+            torch.cuda.current_stream(self.device).wait_event(self._pending_transfer_event)
+            self._pending_transfer_waited = True
+        lens_after = [x - 1 for x in self._pending_new_lens[layer_idx]]  # the append comes next
+        cu_mid = _build_cu_seqlens(lens_after, self.device)
+        k, v = _compact_no_append(self, layer_idx, cu_mid, lens_after)
+        self._finish_layer(layer_idx, k, v, cu_mid, lens_after)
+
+    def _finish_layer(self, layer_idx, k, v, cu_new, new_lens) -> None:
+        self.layer_k[layer_idx], self.layer_v[layer_idx] = k, v
+        self.seq_lens[layer_idx] = list(new_lens)
+        self.cu_seqlens_k[layer_idx] = cu_new
+        self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(new_lens)
+        self._pending_layers_applied += 1
+        if self._pending_layers_applied == self.num_layers:
+            self._pending_chunk_update = False
+            self._clear_pending_rebuild_state()
+
+    # ------------------------------------------------------------------ stats
+    def _snapshot_cache_stats(self, step: int = -1) -> list[dict]:
+        """cache.py:1013-1085 (per-sample GPU/CPU token accounting)."""
+        if self._planner is not None:
+            self.loaded_segments = [set(self._planner.get_loaded_segments(b)) for b in range(self.batch_size)]
+        out = []
+        for b in range(self.batch_size):
+            gpu_total = sum(self.seq_lens[l][b * self.num_kv_heads + h] for l in range(self.num_layers)
+                            for h in range(self.num_kv_heads) if self.seq_lens[l] is not None)
+            cpu_restore = sum(m.cpu_end - m.cpu_start for l in range(self.num_layers)
+                              for h in range(self.num_kv_heads) if self.config.is_class_b(l, h)
+                              for m in self.restore_meta[l][b][h] if m is not None)
+            out.append({"step": step, "gpu_total_tokens": gpu_total, "cpu_restore_tokens": cpu_restore,
+                        "loaded_segments": sorted(self.loaded_segments[b])})
+        return out
+
+    def get_all_stats(self) -> list[dict]:
+        return self.stats.get_all_stats()
+
+    def collect_stats(self, interval: int = 20) -> None:
+        self.stats.set_interval(interval)
+
+
+def _compact_no_append(cache: WnWCache, layer_idx: int, cu_mid: Tensor, lens_after: list[int]):
+    """Compaction + load of one layer without the new row (dense source and
+    destination, every segment listed): the kernel of wnw_compact_segments."""
+    from .kernels import compact_segments
+    N = cache.batch_size * cache.num_kv_heads
+    dev = cache.device
+    old = cache.layer_k[layer_idx]
+    k = torch.empty(sum(lens_after), cache.head_dim, dtype=old.dtype, device=dev)
+    v = torch.empty_like(k)
+    cu_old = cache.cu_seqlens_k[layer_idx]
+    compact_segments(
+        cache.layer_k[layer_idx], cache.layer_v[layer_idx], k, v, torch.arange(N, dtype=torch.int32, device=dev),
+        cu_old[:-1].to(torch.int64), (cu_old[1:] - cu_old[:-1]).to(torch.int32), cu_mid[:-1].to(torch.int64),
+        torch.tensor(lens_after, dtype=torch.int32, device=dev), cache._pending_gpu_k, cache._pending_gpu_v,
+        cache._pending_load_starts[layer_idx], cache._pending_load_lens[layer_idx],
+        cache._pending_evict_offsets[layer_idx], cache._pending_evict_starts[layer_idx],
+        cache._pending_evict_ends[layer_idx], max(lens_after) if lens_after else 0)
+    return k, v

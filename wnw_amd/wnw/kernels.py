@@ -136,3 +136,57 @@ def fused_score_accumulate(
         _lib.ptr(audio_ends), _lib.ptr(accumulator), _lib.ptr(accum_offsets), S, nh, d, K.shape[0],
         accumulator.numel(), int(max_audio), scale, _lib.dtype_code(Q.dtype), _lib.ptr(ws), ws.numel(),
         _lib.stream_of(dev)), "fused_score_accumulate")
+
+
+def compact_segments(
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    seg_list: torch.Tensor,
+    src_base: torch.Tensor,
+    src_len: torch.Tensor,
+    dst_base: torch.Tensor,
+    new_len: torch.Tensor,
+    load_k: torch.Tensor,
+    load_v: torch.Tensor,
+    load_starts: torch.Tensor,
+    load_lens: torch.Tensor,
+    evict_offsets: torch.Tensor,
+    evict_starts: torch.Tensor,
+    evict_ends: torch.Tensor,
+    max_new_len: int,
+    *,
+    new_k: torch.Tensor | None = None,
+    new_v: torch.Tensor | None = None,
+) -> None:
+    """Compaction + load (+ optional append) of the listed segments between
+    physically addressed layouts (``wnw_compact_segments``).  With
+    ``new_k=None`` no row is appended: the compaction step of the reference's
+    out-of-place fallback (src/algorithms/wnw/code/cache.py:891-1010)."""
+    _lib.require_gpu(src_k, src_v, dst_k, dst_v, seg_list, src_base, src_len, dst_base, new_len, load_starts,
+                     load_lens, evict_offsets)
+    n = src_base.numel()
+    d = src_k.shape[1]
+    for name, t, dt in (("seg_list", seg_list, torch.int32), ("src_base", src_base, torch.int64),
+                        ("src_len", src_len, torch.int32), ("dst_base", dst_base, torch.int64),
+                        ("new_len", new_len, torch.int32), ("load_starts", load_starts, torch.int32),
+                        ("load_lens", load_lens, torch.int32), ("evict_offsets", evict_offsets, torch.int32)):
+        if t.dtype != dt:
+            raise _lib.WnwError(f"{name} must be {dt}")
+    if evict_offsets.numel() != n + 1:
+        raise _lib.WnwError("evict_offsets must be int32 [N+1]")
+    with_new = new_k is not None
+    keep = [t.contiguous() if t is not None and t.numel() else None for t in
+            (new_k, new_v, load_k, load_v, seg_list, src_base, src_len, dst_base, new_len, load_starts, load_lens,
+             evict_offsets, evict_starts, evict_ends)]
+    nk, nv, lk, lv, sl, sb, sn, db, nl, ls, ll, eo, es, ee = keep
+    n_ev = 0 if es is None else es.numel()
+    _lib.ensure_init(src_k.device)
+    _lib.check(_lib.lib().wnw_compact_segments(
+        _lib.ptr(src_k), _lib.ptr(src_v), _lib.ptr(dst_k), _lib.ptr(dst_v), _lib.ptr(nk), _lib.ptr(nv),
+        _lib.ptr(lk), _lib.ptr(lv), _lib.ptr(sl), seg_list.numel(), n, int(max_new_len), _lib.ptr(sb),
+        _lib.ptr(sn), _lib.ptr(db), _lib.ptr(nl), _lib.ptr(ls), _lib.ptr(ll), _lib.ptr(eo), _lib.ptr(es),
+        _lib.ptr(ee), n_ev, 1 if with_new else 0, src_k.shape[0], dst_k.shape[0],
+        0 if lk is None else lk.shape[0], d, _lib.dtype_code(src_k.dtype), _lib.stream_of(src_k.device)),
+        "compact_segments")
