@@ -156,7 +156,7 @@ def q1_decode_attn_score(
     """Attention output [nseg, G, D] plus class-A score accumulation.
 
     Reference: ``q1_decode_attn_score`` (src/common/kv/fused_attn.py:
-    126-156): for every segment whose KV head is flagged in ``ca_kv_mask``,
+    124-156): for every segment whose KV head is flagged in ``ca_kv_mask``,
     each audio token's softmax weight summed over the group's query heads is
     added to ``score_accumulator[score_offsets[b] + token]``.  The weights
     use the attention's own final softmax statistics.  ``max_audio`` (the
