@@ -47,9 +47,11 @@ extern "C" {
 #define WNW_DEVERR_CAPACITY 4 /* in-place append beyond segment capacity   */
 
 /* attention kernel selection (wnw_decode_attn_ex) */
-#define WNW_ATTN_AUTO 0 /* MFMA kernel where supported, else VALU kernel  */
+#define WNW_ATTN_AUTO 0 /* fastest kernel that supports the arguments    */
 #define WNW_ATTN_MFMA 1 /* bf16/f16, head_dim 64/128, group <= 16         */
 #define WNW_ATTN_VALU 2 /* any dtype, head_dim 64/128/256, group <= 16    */
+#define WNW_ATTN_STREAM 3 /* bf16/f16, head_dim 64/128, group <= 8 (AUTO's
+                             choice there)                              */
 
 /* Message describing the last failure on this thread ("" if none). */
 const char* wnw_last_error(void);

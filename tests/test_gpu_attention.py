@@ -50,10 +50,12 @@ def _run_case(dev, lens, G, D, dtype, kernel="auto", n_wg=0, scale=None, seed=0,
     return got, ref
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("kernel", ["stream", "mfma", "valu"])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
-@pytest.mark.parametrize("G", [1, 4, 7, 16])
+@pytest.mark.parametrize("G", [1, 4, 7, 8, 16])
 def test_small_ragged(gpu, kernel, dtype, G):
+    if kernel == "stream" and G > 8:
+        pytest.skip("the streaming kernel takes groups of up to 8 heads")
     lens = [1, 2, 31, 32, 33, 64, 100, 257, 0, 5, 1000, 3]
     got, ref = _run_case(gpu, lens, G, 128, dtype, kernel=kernel, seed=G)
     ok, msg = allclose_report(got, ref, *_tol(dtype))
@@ -61,9 +63,10 @@ def test_small_ragged(gpu, kernel, dtype, G):
     assert np.all(got[8] == 0)  # empty segment
 
 
+@pytest.mark.parametrize("kernel", ["stream", "mfma"])
 @pytest.mark.parametrize("D", [64, 128])
-def test_head_dims(gpu, D):
-    got, ref = _run_case(gpu, [70, 1, 300, 129], 4, D, "bfloat16", seed=11)
+def test_head_dims(gpu, D, kernel):
+    got, ref = _run_case(gpu, [70, 1, 300, 129], 4, D, "bfloat16", seed=11, kernel=kernel)
     ok, msg = allclose_report(got, ref, ATOL, RTOL)
     assert ok, msg
 
@@ -74,11 +77,12 @@ def test_valu_head_dim_256(gpu):
     assert ok, msg
 
 
+@pytest.mark.parametrize("kernel", ["stream", "mfma"])
 @pytest.mark.parametrize("n_wg", [1, 2, 3, 7, 64, 333, 2048])
-def test_split_counts_agree(gpu, n_wg):
+def test_split_counts_agree(gpu, n_wg, kernel):
     """Any stream-K split must give the no-split result (log-sum-exp merge identity)."""
     lens = [513, 7565, 1, 90, 2048, 4]
-    got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", n_wg=n_wg, seed=5)
+    got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", n_wg=n_wg, seed=5, kernel=kernel)
     ok, msg = allclose_report(got, ref, ATOL, RTOL)
     assert ok, msg
 
@@ -219,3 +223,23 @@ def test_bad_offsets_are_refused_not_read(gpu):
     got, ref = _run_case(gpu, [50, 60], 4, 128, "bfloat16", seed=40)
     ok, msg = allclose_report(got, ref, ATOL, RTOL)
     assert ok, msg
+
+
+@pytest.mark.parametrize("kernel", ["stream", "mfma"])
+def test_many_tiny_segments(gpu, kernel):
+    """More than 64 segments in one workgroup's range (segment bounds read
+    from global memory instead of the LDS ring), lengths 0..3."""
+    rng = np.random.default_rng(41)
+    lens = rng.integers(0, 4, size=900)
+    got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", kernel=kernel, seed=41, n_wg=3)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("lens", [[17], [16, 16, 16, 16], [15, 1, 33, 64, 5], [1000, 1, 1, 1000]])
+def test_stream_step_boundaries(gpu, lens):
+    """Pieces ending mid-step, single-row pieces and exact multiples of the 16-row step."""
+    for n_wg in (1, 2, 5):
+        got, ref = _run_case(gpu, lens, 7, 128, "bfloat16", kernel="stream", seed=len(lens) + n_wg, n_wg=n_wg)
+        ok, msg = allclose_report(got, ref, ATOL, RTOL)
+        assert ok, msg

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwnw_amd.
 
 WNW_OK, WNW_EINVAL, WNW_EHIP, WNW_ENOTSUP = 0, 1, 2, 3
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
-ATTN_AUTO, ATTN_MFMA, ATTN_VALU = 0, 1, 2
+ATTN_AUTO, ATTN_MFMA, ATTN_VALU, ATTN_STREAM = 0, 1, 2, 3
 DEVERR_BOUNDS, DEVERR_ORDER, DEVERR_CAPACITY = 1, 2, 4
 
 _TORCH_DTYPES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}

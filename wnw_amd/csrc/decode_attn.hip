@@ -120,6 +120,13 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       }
     }
   };
+  // Ring entries are written only for segments that overlap this range;
+  // an empty or invalid segment between s_first and s_last must read as
+  // empty (length 0), not as what an earlier kernel left in LDS.
+  if (tid < kRing) {
+    sl.ring_base[tid] = 0;
+    sl.ring_len[tid] = 0;
+  }
   // The loads of the first chunk are issued before the barrier: one global
   // round trip for n_seg <= 4 * NT.
   load_chunk(0);
@@ -143,13 +150,13 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       if (len == 0 || b < 0 || b + len > R) {
         if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
         if (owner) {
-          T* o = (T*)p.out + (int64_t)i * p.G * D;
           const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
-          for (int e = 0; e < p.G * D; ++e) Elem<T>::store(o, e, fill);
+          for (int e = 0; e < p.G * D; ++e) store_elem<T>(p.out, (int64_t)i * p.G * D + e, fill);
           if (p.lse) {
+            WNW_GLOBAL float* ls = gptr_w<float>(p.lse) + (int64_t)i * p.G * 2;
             for (int g = 0; g < p.G; ++g) {
-              p.lse[((int64_t)i * p.G + g) * 2] = len == 0 ? kNegBig : fill;
-              p.lse[((int64_t)i * p.G + g) * 2 + 1] = len == 0 ? 0.f : fill;
+              ls[2 * g] = len == 0 ? kNegBig : fill;
+              ls[2 * g + 1] = len == 0 ? 0.f : fill;
             }
           }
         }
@@ -222,10 +229,14 @@ __device__ __forceinline__ Piece make_piece(const AttnParams& p, const SchedLds&
 // XCD is visible to a reader on another without any L2 write-back or
 // invalidation of the whole cache (which a release/acquire fence costs).
 __device__ __forceinline__ void st_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gptr_w<float>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void st_agent2(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(gptr_w<uint64_t>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent2(const float* p) {
+  return __hip_atomic_load(gptr_w<uint64_t>(const_cast<float*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // s_waitcnt vmcnt(0): every vector memory access of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -236,93 +247,104 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N & 0x30) << 10));
 }
 
-// Last-arriver merge of the np partials of one segment (slots s0 .. s0+np-1)
-// into the output.  The partials of consecutive slots are contiguous, so a
-// chunk of pieces is one contiguous block of accumulators and one of (m, l)
-// pairs: both are copied straight into LDS with agent-coherent (sc1) direct
-// global->LDS loads, one memory round trip per chunk and almost no
-// registers.  Per head, a wave reduces the chunk's maxima and sums across
-// its lanes (one piece per lane); then every thread folds its output
-// elements over the chunk.  Summation order is fixed, so results are
-// deterministic.  `lds` / `lds_bytes` is the workgroup's LDS, free here.
-template <typename T, int NT>
-__device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, T* o,
-                                               float* lse, uint8_t* lds, int lds_bytes) {
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
+// Last-arriver merge of the np partials of one segment (slots s0 ..
+// s0 + np - 1) into the output, by threads t = 0 .. nt - 1.  Every thread
+// owns 4 consecutive elements of one head and reads, for a chunk of partials
+// at a time, their (m, l) pairs and its accumulator quad with agent-coherent
+// loads: one memory round trip per chunk, no LDS and no barriers.  Chunks
+// are folded in slot order with the usual max rescaling, so the result is
+// deterministic.
+template <typename T>
+__device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, int64_t s, int t,
+                                               int nt) {
+  constexpr int QC = 16;  // partials per round trip
   const int G = p.G;
   const int GD = G * D;
-  float* gm = (float*)lds;                    // [3][16]: M, L, rescale per head
-  float* wml = gm + 3 * kMaxGroup;            // [pch][G][2]: (m, l), then (weight, l)
-  const int head = 3 * kMaxGroup * 4;         // bytes before the (m, l) table
-  // pieces per chunk (at most one per lane): (m, l) table (8 * G bytes each)
-  // + accumulators (4 * GD bytes each), 1 KB of alignment slack
-  const int room = (lds_bytes - head - 2048) / (4 * GD + 8 * G);
-  const int pch = max(1, min(min(np, room), 64));
-  // 1 KB aligned.  The offset is rounded as an integer so that the pointer
-  // keeps its LDS address space (a round trip through uintptr_t would make
-  // every access a FLAT one, which forces full memory waits).
-  uint8_t* accl = lds + ((head + 8 * pch * G + 1023) & ~1023);  // [pch][GD]
-  const int ept = (GD + NT - 1) / NT;
-  float accv[kMaxGroup * 256 / 256];          // up to 16 elements per thread (G * D <= 4096)
+  const int GD4 = GD / 4;
+  for (int i4 = t; i4 < GD4; i4 += nt) {
+    const int g = (4 * i4) / D;
+    float M = kNegBig, L = 0.f;
+    f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q0 = 0; q0 < np; q0 += QC) {
+      uint64_t ml[QC], a01[QC], a23[QC];
 #pragma unroll
-  for (int e = 0; e < kMaxGroup * 256 / 256; ++e) accv[e] = 0.f;
-  for (int q0 = 0; q0 < np; q0 += pch) {
-    const int nq = min(pch, np - q0);
-    // accumulators: nq * GD floats, 1 KB per wave-wide 16-byte load
-    const int nvec = nq * GD / 4;
-    const WNW_GLOBAL float* src = gptr<float>(p.part_acc + (s0 + q0) * GD);
-    for (int k = w; k * 64 < nvec; k += NT / 64) {
-      const int v = k * 64 + lane;
-      if (v < nvec) __builtin_amdgcn_global_load_lds(src + 4 * v, accl + k * 1024, 16, 0, 16 /* sc1 */);
-    }
-    // (m, l) pairs: nq * G * 2 floats, 256 B per wave-wide 4-byte load
-    const int nml = nq * G * 2;
-    const WNW_GLOBAL float* srcm = gptr<float>(p.part_ml + (s0 + q0) * G * 2);
-    for (int k = w; k * 64 < nml; k += NT / 64) {
-      const int v = k * 64 + lane;
-      if (v < nml) __builtin_amdgcn_global_load_lds(srcm + v, (uint8_t*)wml + k * 256, 4, 0, 16 /* sc1 */);
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    // wave w takes heads w, w + NW, ...; lane q holds piece q of the chunk
-    for (int g = w; g < G; g += NT / 64) {
-      const float M = q0 == 0 ? kNegBig : gm[g];
-      const float mq = lane < nq ? wml[(lane * G + g) * 2] : kNegBig;
-      const float Mn = fmaxf(M, wave_max(mq));
-      const float wq = lane < nq ? exp2f(mq - Mn) : 0.f;
-      const float lsum = wave_sum(lane < nq ? wml[(lane * G + g) * 2 + 1] * wq : 0.f);
-      if (lane < nq) wml[(lane * G + g) * 2] = wq;
-      if (lane == 0) {
-        const float so = exp2f(M - Mn);
-        gm[kMaxGroup + g] = (q0 == 0 ? 0.f : gm[kMaxGroup + g]) * so + lsum;
-        gm[2 * kMaxGroup + g] = so;
-        gm[g] = Mn;
+      for (int k = 0; k < QC; ++k) {
+        const int64_t slot = s0 + min(q0 + k, np - 1);  // past np: a repeat, masked below
+        ml[k] = ld_agent2(p.part_ml + (slot * G + g) * 2);
+        a01[k] = ld_agent2(p.part_acc + slot * GD + 4 * i4);
+        a23[k] = ld_agent2(p.part_acc + slot * GD + 4 * i4 + 2);
       }
-    }
-    __syncthreads();
-    const float* acl = (const float*)accl;
-    for (int e = 0; e < ept; ++e) {
-      const int idx = tid + e * NT;
-      if (idx < GD) {
-        const int g = idx / D;
-        float a = accv[e] * gm[2 * kMaxGroup + g];
-#pragma unroll 8
-        for (int q = 0; q < nq; ++q) a += acl[q * GD + idx] * wml[(q * G + g) * 2];
-        accv[e] = a;
+      float Mc = M;
+#pragma unroll
+      for (int k = 0; k < QC; ++k)
+        if (q0 + k < np) Mc = fmaxf(Mc, __uint_as_float((uint32_t)ml[k]));
+      const float so = exp2f(M - Mc);
+      L *= so;
+      A *= so;
+#pragma unroll
+      for (int k = 0; k < QC; ++k) {
+        if (q0 + k >= np) continue;
+        const float wk = exp2f(__uint_as_float((uint32_t)ml[k]) - Mc);
+        L += __uint_as_float((uint32_t)(ml[k] >> 32)) * wk;
+        A += f32x4{__uint_as_float((uint32_t)a01[k]), __uint_as_float((uint32_t)(a01[k] >> 32)),
+                   __uint_as_float((uint32_t)a23[k]), __uint_as_float((uint32_t)(a23[k] >> 32))} *
+             wk;
       }
+      M = Mc;
     }
-    __syncthreads();
+    const float inv = 1.f / L;
+    const int64_t e0 = s * GD + 4 * i4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_elem<T>(p.out, e0 + i, A[i] * inv);
+    if (p.lse && (4 * i4) % D == 0) {
+      gptr_w<float>(p.lse)[(s * G + g) * 2] = M;
+      gptr_w<float>(p.lse)[(s * G + g) * 2 + 1] = L;
+    }
   }
-  for (int e = 0; e < ept; ++e) {
-    const int idx = tid + e * NT;
-    if (idx < GD) Elem<T>::store(o, idx, accv[e] / gm[kMaxGroup + idx / D]);
-  }
-  if (lse && tid < G) {
-    lse[tid * 2] = gm[tid];
-    lse[tid * 2 + 1] = gm[kMaxGroup + tid];
-  }
+}
+
+// Pieces (workgroups) of the segment at [seg_base, seg_base + seg_len).
+__device__ __forceinline__ void piece_range(const SchedLds& sl, int64_t seg_base, int64_t seg_len, int64_t& p_first,
+                                            int64_t& p_last) {
+  const int64_t R = sl.R, P = sl.P;
+  p_first = min(max(owner_of(seg_base, R, P), (int64_t)0), P - 1);
+  p_last = min(max(owner_of(seg_base + seg_len - 1, R, P), p_first), P - 1);
+}
+
+// Arrival of this workgroup's partial of segment s (already written with
+// agent-coherent stores and waited for, followed by a barrier): bump the
+// segment's counter and return whether this was the last piece.  One thread.
+__device__ __forceinline__ bool arrive(const AttnParams& p, const SchedLds& sl, int64_t seg_base, int64_t seg_len,
+                                      int s) {
+  int64_t p_first, p_last;
+  piece_range(sl, seg_base, seg_len, p_first, p_last);
+  const int old =
+      __hip_atomic_fetch_add(gptr_w<int32_t>(p.counters) + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return old == (int)(p_last - p_first);
+}
+
+// The last arriver of segment s merges every partial into the output (by
+// threads t = 0 .. nt - 1 of the workgroup) and resets the counter for the
+// next launch.  No LDS is used.
+template <typename T>
+__device__ __forceinline__ void combine_segment(const AttnParams& p, int D, const SchedLds& sl, int64_t seg_base,
+                                                int64_t seg_len, int s, int t, int nt) {
+  int64_t p_first, p_last;
+  piece_range(sl, seg_base, seg_len, p_first, p_last);
+  const int np = (int)(p_last - p_first + 1);
+  combine_pieces<T>(p, D, p_first + s /* slot of the first piece */, np, s, t, nt);
+  if (t == 0) __hip_atomic_store(gptr_w<int32_t>(p.counters) + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival of this workgroup's partial of segment s followed, on the last
+// arrival, by the merge.  Called by all threads.
+template <typename T, int NT>
+__device__ __forceinline__ void arrive_and_combine(const AttnParams& p, int D, SchedLds& sl, int64_t seg_base,
+                                                   int64_t seg_len, int s) {
+  if (threadIdx.x == 0) sl.is_last = arrive(p, sl, seg_base, seg_len, s);
+  __syncthreads();
+  if (!sl.is_last) return;  // workgroup-uniform
+  combine_segment<T>(p, D, sl, seg_base, seg_len, s, threadIdx.x, NT);
 }
 
 // Merge the NW wave states in LDS (layout: ml[w][g] = (m, l),
@@ -338,7 +360,7 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
 // the next launch.
 template <typename T, int NT, int NW>
 __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLds& sl, const Piece& pc, int s,
-                                             float* mrg_ml, float* mrg_acc, uint8_t* lds, int lds_bytes) {
+                                             float* mrg_ml, float* mrg_acc) {
   const int tid = threadIdx.x;
   const int G = p.G;
   const int GD = G * D;
@@ -356,10 +378,10 @@ __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLd
         L += mrg_ml[(w * kMaxGroup + g) * 2 + 1] * sc;
         A += mrg_acc[(w * kMaxGroup + g) * D + (idx - g * D)] * sc;
       }
-      Elem<T>::store(o, idx, A / L);
+      store_elem<T>(o, idx, A / L);
       if (p.lse && idx - g * D == 0) {
-        p.lse[((int64_t)s * G + g) * 2] = M;
-        p.lse[((int64_t)s * G + g) * 2 + 1] = L;
+        gptr_w<float>(p.lse)[((int64_t)s * G + g) * 2] = M;
+        gptr_w<float>(p.lse)[((int64_t)s * G + g) * 2 + 1] = L;
       }
     }
     __syncthreads();  // LDS reuse by the next piece
@@ -388,22 +410,7 @@ __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLd
   }
   wait_vmem();
   __syncthreads();
-  const int64_t R = sl.R, P = sl.P;
-  const int64_t p_first = min(max(owner_of(pc.seg_base, R, P), (int64_t)0), P - 1);
-  const int64_t p_last = min(max(owner_of(pc.seg_base + pc.seg_len - 1, R, P), p_first), P - 1);
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(&p.counters[s], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sl.is_last = (old == (int)(p_last - p_first));
-  }
-  __syncthreads();
-  if (!sl.is_last) return;  // workgroup-uniform
-
-  T* o = (T*)p.out + (int64_t)s * GD;
-  const int np = (int)(p_last - p_first + 1);
-  const int64_t s0 = p_first + s;  // slot of the first piece
-  combine_pieces<T, NT>(p, D, s0, np, o, p.lse ? p.lse + (int64_t)s * G * 2 : nullptr, lds, lds_bytes);
-  if (tid == 0) __hip_atomic_store(&p.counters[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
+  arrive_and_combine<T, NT>(p, D, sl, pc.seg_base, pc.seg_len, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -667,9 +674,546 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_mfma_kernel(AttnParams p) {
         *(f32x4*)(mrg_acc + (w * kMaxGroup + lc) * D + 16 * t + 4 * lq) = acc[t];
     }
     __syncthreads();
-    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc, lds, MfmaLds<D, NW>::kBytes);
+    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc);
   }
   wait_vmcnt<0>();
+}
+
+// ---------------------------------------------------------------------------
+// Streaming MFMA kernel (bf16 / f16 K, V, q; D = 64 or 128; G <= 8)
+// ---------------------------------------------------------------------------
+// Each wave owns a contiguous quarter of its workgroup's row range and walks
+// the segments overlapping it in 16-row steps, two steps in flight, without
+// stopping at segment boundaries.  The K and V rows and the segment's q of a
+// step are copied straight into the wave's LDS buffers by direct global->LDS
+// loads issued from inline assembly, so the compiler tracks none of them and
+// inserts no memory waits of its own; every wait below is explicit, with a
+// count fixed per step (K, q, V: NI + QD + NI loads, in that order).
+//
+// Per step (16 rows):
+//   S^T (16 rows x 16 heads) = K_tile x q^T: D/32 v_mfma_f32_16x16x32, the
+//       K operand read row by row from LDS (16-byte chunks XOR-swizzled by
+//       the row, so the 16 rows of one read hit distinct banks);
+//   O^T += V^T x P^T: D/16 tiles of v_mfma_f32_16x16x16, two per tile (P
+//       split into hi + lo halves); the V^T operand comes from one
+//       ds_read_b64_tr_b16 per lane and tile (4 rows x 1 column each),
+//       and the S output layout is already the P^T operand layout.
+// A segment that lies entirely inside the wave's range is finished in the
+// stream (output written at once).  Only a wave's first and last pieces can
+// be shared; their states are kept in registers and merged through LDS after
+// the stream, then written as an output, or as a workgroup partial that the
+// last-arriver protocol combines.
+static constexpr int kSRows = 16;    // rows per step
+static constexpr int kMaxGroupS = 8;  // heads per group of this kernel
+
+// 16 bytes per lane from gbase + voff into LDS at lds_addr + 16 * lane.
+// M0 carries the LDS address; it is saved and restored around the load, so
+// the compiler's own uses of M0 are unaffected.
+__device__ __forceinline__ void dma_copy16(const void* gbase, uint32_t voff, uint32_t lds_addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "global_load_lds_dwordx4 %1, %2 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(voff), "s"(gbase), "s"(lds_addr)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <typename T>
+struct StreamOps;
+template <>
+struct StreamOps<bf16_t> {
+  typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  __device__ static f32x4 qk(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  __device__ static uint64_t vt(const uint8_t* lds) {
+    return __builtin_bit_cast(uint64_t,
+                              __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) v4*)lds));
+  }
+  __device__ static f32x4 pv(uint64_t a, uint64_t b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0,
+                                                     0);
+  }
+  __device__ static uint32_t from_f32(float x) { return f32_to_bf16_bits(x); }
+  __device__ static float to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+};
+template <>
+struct StreamOps<f16_t> {
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
+  typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+  __device__ static f32x4 qk(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+  __device__ static uint64_t vt(const uint8_t* lds) {
+    return __builtin_bit_cast(uint64_t,
+                              __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4*)lds));
+  }
+  __device__ static f32x4 pv(uint64_t a, uint64_t b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4, a), __builtin_bit_cast(v4, b), c, 0, 0, 0);
+  }
+  __device__ static uint32_t from_f32(float x) { return f32_to_f16_bits(x); }
+  __device__ static float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
+};
+
+template <int D>
+struct StreamGeom {
+  static constexpr int RB = D * 2;             // bytes per row
+  static constexpr int SB = kSRows * RB;       // bytes per tensor per step
+  static constexpr int NI = SB / 1024;         // 1 KB loads per tensor per step
+  static constexpr int RPI = 1024 / RB;        // rows per load
+  static constexpr int CH = RB / 16;           // 16-byte chunks per row
+  static constexpr int NC = D / 32;            // QK k-chunks
+  static constexpr int NTD = D / 16;           // PV output tiles
+  static constexpr int kSlot = 16 + 2 * kMaxGroupS * 4 + kMaxGroupS * D * 4;  // merge slot bytes
+};
+
+// LDS bytes of the streaming kernel: per wave two (K, V) step buffers and two
+// q slots of qslot bytes; the merge slots reuse the step buffers.
+__host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot) {
+  return NW * (4 * kSRows * D * 2 + 2 * qslot);
+}
+
+// One step of a wave's stream: rows [row0, row0 + nrows) of segment s.
+struct SStep {
+  int64_t row0;
+  int64_t seg_b;
+  int32_t s, nrows, seg_len, qslot;
+  int32_t first, last, whole;
+};
+
+template <typename T, int D, int NW, int QD>
+__global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
+  using G_ = StreamGeom<D>;
+  using Ops = StreamOps<T>;
+  constexpr int NT = NW * 64;
+  constexpr int RB = G_::RB, SB = G_::SB, NI = G_::NI, RPI = G_::RPI, CH = G_::CH, NC = G_::NC, NTD = G_::NTD;
+  constexpr int E = NI + QD + NI;  // loads per step
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  __shared__ SchedLds sl;
+
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int lq = lane >> 4, lc = lane & 15;
+  const int G = p.G;
+  const int qbytes = G * RB;
+  const int qslot = (qbytes + 255) & ~255;
+
+  // the per-step load count (E) must match the group: q takes exactly QD loads
+  if (QD != (qbytes + 1023) / 1024) {
+    if (tid == 0 && blockIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    return;
+  }
+  uint8_t* wbuf = dyn + w * 4 * SB;                    // K0 V0 K1 V1
+  uint8_t* qbuf = dyn + NW * 4 * SB + w * 2 * qslot;   // q slot 0, 1
+  const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_address(wbuf));
+  const uint32_t lds_q = __builtin_amdgcn_readfirstlane(lds_address(qbuf));
+  const T* kp = (const T*)p.k;
+  const T* vp = (const T*)p.v;
+  // rows [row0, row0 + nrows) of K or V into step buffer b, 16-byte chunks
+  // swizzled by the row (K: chunk ^ (r % CH); V: chunk ^ 2 (r % 4)); rows past
+  // nrows repeat the last row
+  auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b) {
+    const T* src = (is_v ? vp : kp) + row0 * D;
+    const uint32_t dst = lds_w + b * 2 * SB + (is_v ? SB : 0);
+#pragma unroll
+    for (int u = 0; u < NI; ++u) {
+      const int r = u * RPI + lane / CH;
+      const int rr = max(0, r < nrows ? r : nrows - 1);
+      const int sw = is_v ? 2 * (r & 3) : r % CH;
+      dma_copy16(src, (uint32_t)(rr * RB + (((lane % CH) ^ sw) * 16)), dst + u * 1024);
+    }
+  };
+  schedule<T, NT>(p, D, sl);
+  if (sl.s_first > sl.s_last) return;
+  const int64_t R = uni(sl.R);
+  const int64_t B0 = uni(sl.B0), B1 = uni(sl.B1);
+  const int64_t W0 = B0 + (B1 - B0) * w / NW, W1 = B0 + (B1 - B0) * (w + 1) / NW;
+  const int s_first = uni(sl.s_first), s_last = uni(sl.s_last);
+  const bool in_ring = (s_last - s_first) < kRing;
+
+  // ---- segment walk: a window of 64 segments, one per lane; the mask holds
+  // the valid ones overlapping [W0, W1) that are not taken yet.
+  int wb = s_first;
+  int64_t lb = 0;
+  int32_t llen = 0;
+  uint64_t mask = 0;
+  auto load_window = [&]() {
+    const int s = wb + lane;
+    lb = 0;
+    llen = 0;
+    if (s <= s_last) {
+      if (in_ring) {
+        lb = sl.ring_base[s % kRing];
+        llen = sl.ring_len[s % kRing];
+      } else {
+        const int32_t lo = p.cu[s], hi = p.cu[s + 1];
+        lb = p.base ? p.base[s] : (int64_t)lo;
+        llen = hi - lo;
+      }
+    }
+    // the piece [max(lb, W0), min(lb + len, W1)) must be non-empty (an empty
+    // wave range inside a segment overlaps nothing)
+    const bool ov = s <= s_last && llen > 0 && lb >= 0 && lb + llen <= R && max(lb, W0) < min(lb + llen, W1);
+    mask = __ballot(ov);
+  };
+  load_window();
+  // issue-side iterator: current piece [pb, pe) of segment cur_s
+  int cur_s = 0, cur_len = 0, piece_no = 0;
+  int64_t cur_b = 0, pb = 0, pe = 0, irow = 0;
+  bool cur_whole = false, have = false;
+  auto next_piece = [&]() {
+    while (mask == 0) {
+      wb += 64;
+      if (wb > s_last) {
+        have = false;
+        return;
+      }
+      load_window();
+    }
+    const int k = __builtin_ctzll(mask);
+    mask &= mask - 1;
+    cur_s = wb + k;
+    const uint32_t blo = __builtin_amdgcn_readlane((uint32_t)lb, k);
+    const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)lb >> 32), k);
+    cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
+    cur_len = __builtin_amdgcn_readlane(llen, k);
+    pb = max(cur_b, W0);
+    pe = min(cur_b + cur_len, W1);
+    cur_whole = cur_b >= W0 && cur_b + cur_len <= W1;
+    irow = pb;
+    have = true;
+  };
+  next_piece();
+  auto gen = [&](SStep& st) -> bool {
+    if (!have) return false;
+    st.s = cur_s;
+    st.seg_b = cur_b;
+    st.seg_len = cur_len;
+    st.row0 = irow;
+    st.nrows = (int32_t)min((int64_t)kSRows, pe - irow);
+    st.first = irow == pb;
+    st.whole = cur_whole;
+    st.qslot = piece_no & 1;
+    irow += kSRows;
+    st.last = irow >= pe;
+    if (st.last) {
+      ++piece_no;
+      next_piece();
+    }
+    return true;
+  };
+
+  // ---- loads of one step into buffer b: K, q, V (E loads, in this order)
+  auto issue = [&](const SStep& st, int b) {
+    load_rows(false, st.row0, st.nrows, b);
+    const T* qs = (const T*)p.q + (int64_t)st.s * G * D;
+#pragma unroll
+    for (int u = 0; u < QD; ++u) {
+      const int off = u * 1024 + lane * 16;
+      if (off < qbytes) dma_copy16(qs, (uint32_t)off, lds_q + st.qslot * qslot + u * 1024);
+    }
+    load_rows(true, st.row0, st.nrows, b);
+  };
+
+  // ---- softmax state of the current piece, and the held (first, shared) one
+  float m_run = kNegBig, l_run = 0.f;
+  f32x4 acc[NTD];
+  float m_h = kNegBig, l_h = 0.f;
+  f32x4 acc_h[NTD];
+  int32_t h_s = -1, h_len = 0;
+  int64_t h_b = 0;
+#pragma unroll
+  for (int t = 0; t < NTD; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc_h[t] = acc[t];
+  }
+  int32_t c_s = -1, c_len = 0;  // the unfinished piece at the end of the stream
+  int64_t c_b = 0;
+  u32x4 qb[NC];
+
+  auto process = [&](const SStep& st, int b, bool has_next) {
+    uint8_t* kbuf = wbuf + b * 2 * SB;
+    uint8_t* vbuf = kbuf + SB;
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next)
+      wait_vmcnt<NI + E>();
+    else
+      wait_vmcnt<NI>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (st.first) {  // q of this piece: operand lane (lq, lc) = q[g = lc][32c + 8lq ..]
+      const uint8_t* qsl = qbuf + st.qslot * qslot;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        qb[c] = lc < G ? *(const u32x4*)(qsl + lc * RB + (4 * c + lq) * 16) : u32x4{0, 0, 0, 0};
+    }
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const u32x4 a = *(const u32x4*)(kbuf + lc * RB + (((4 * c + lq) ^ (lc % CH)) * 16));
+      sacc = Ops::qk(a, qb[c], sacc);
+    }
+    // online softmax for head g = lc over rows 4 lq + i
+    float x[4];
+    float mx = kNegBig;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = (4 * lq + i) < st.nrows ? sacc[i] * p.scale_log2 : -INFINITY;
+      mx = fmaxf(mx, x[i]);
+    }
+    mx = fmaxf(mx, swap16(mx));
+    mx = fmaxf(mx, swap32(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    uint32_t hb[4], lo[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pv = exp2f(x[i] - m_new);
+      psum += pv;
+      hb[i] = Ops::from_f32(pv);
+      lo[i] = Ops::from_f32(pv - Ops::to_f32(hb[i]));
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int t = 0; t < NTD; ++t) acc[t] *= alpha;
+    const uint64_t ph = (uint64_t)(hb[0] | (hb[1] << 16)) | ((uint64_t)(hb[2] | (hb[3] << 16)) << 32);
+    const uint64_t pl = (uint64_t)(lo[0] | (lo[1] << 16)) | ((uint64_t)(lo[2] | (lo[3] << 16)) << 32);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next)
+      wait_vmcnt<E>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    // V^T operand of tile t: lane (lq, lc) addresses row 4 lq + lc / 4, columns
+    // 16 t + 4 (lc % 4) .. + 3 (8 bytes of the swizzled row)
+    {
+      const int r = 4 * lq + (lc >> 2);
+      const int sw = 2 * (r & 3);
+      const uint8_t* rowp = vbuf + r * RB + (lc & 1) * 8;
+#pragma unroll
+      for (int t = 0; t < NTD; ++t) {
+        const int chunk = (2 * t + ((lc & 3) >> 1)) ^ sw;
+        const uint64_t a = Ops::vt(rowp + chunk * 16);
+        acc[t] = Ops::pv(a, ph, acc[t]);
+        acc[t] = Ops::pv(a, pl, acc[t]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (st.last) {
+      float l_tot = l_run + swap16(l_run);
+      l_tot += swap32(l_tot);
+      if (st.whole) {  // the segment lies inside this wave's range: finish it
+        if (lc < G) {
+          WNW_GLOBAL uint16_t* o = gptr_w<uint16_t>(p.out) + ((int64_t)st.s * G + lc) * D;
+          const float inv = 1.f / l_tot;
+#pragma unroll
+          for (int t = 0; t < NTD; ++t) {
+            const uint32_t w0 = Ops::from_f32(acc[t][0] * inv) | (Ops::from_f32(acc[t][1] * inv) << 16);
+            const uint32_t w1 = Ops::from_f32(acc[t][2] * inv) | (Ops::from_f32(acc[t][3] * inv) << 16);
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            *(WNW_GLOBAL u32x2*)(o + 16 * t + 4 * lq) = u32x2{w0, w1};
+          }
+          if (p.lse && lq == 0) {
+            WNW_GLOBAL float* ls = gptr_w<float>(p.lse) + ((int64_t)st.s * G + lc) * 2;
+            ls[0] = m_run;
+            ls[1] = l_tot;
+          }
+        }
+      } else if (h_s < 0) {  // first shared piece: hold it until the end
+        h_s = st.s;
+        h_b = st.seg_b;
+        h_len = st.seg_len;
+        m_h = m_run;
+        l_h = l_tot;
+#pragma unroll
+        for (int t = 0; t < NTD; ++t) acc_h[t] = acc[t];
+      } else {  // last shared piece: it is the end of this wave's range
+        c_s = st.s;
+        c_b = st.seg_b;
+        c_len = st.seg_len;
+        l_run = l_tot;
+        return;
+      }
+      m_run = kNegBig;
+      l_run = 0.f;
+#pragma unroll
+      for (int t = 0; t < NTD; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // ---- the stream: two steps in flight (buffers 0 and 1 alternate)
+  SStep sA, sB;
+  bool hA = gen(sA);
+  if (hA) issue(sA, 0);
+  bool hB = hA && gen(sB);
+  if (hB) issue(sB, 1);
+  while (hA) {
+    process(sA, 0, hB);
+    hA = hB && gen(sA);  // the step after sB
+    if (hA) issue(sA, 0);
+    if (!hB) break;
+    process(sB, 1, hA);
+    hB = hA && gen(sB);
+    if (hB) issue(sB, 1);
+    if (!hA) break;
+  }
+  wait_vmcnt<0>();
+
+  // ---- shared pieces: merge the waves' states through LDS
+  __syncthreads();  // every wave is done with its step buffers (reused below)
+  constexpr int SLOT = G_::kSlot;
+  auto slot_of = [&](int i) { return dyn + i * SLOT; };
+  auto put = [&](int i, int32_t s, int64_t b, int32_t len, float m, float l, const f32x4* a) {
+    uint8_t* sp = slot_of(i);
+    if (lane == 0) {
+      *(int32_t*)sp = s;
+      *(int32_t*)(sp + 4) = len;
+      *(int64_t*)(sp + 8) = b;
+    }
+    if (s >= 0 && lc < G) {
+      float* ml = (float*)(sp + 16);
+      if (lq == 0) {
+        ml[lc] = m;
+        ml[kMaxGroupS + lc] = l;
+      }
+      float* ap = (float*)(sp + 16 + 2 * kMaxGroupS * 4) + lc * D;
+#pragma unroll
+      for (int t = 0; t < NTD; ++t) *(f32x4*)(ap + 16 * t + 4 * lq) = a[t];
+    }
+  };
+  put(2 * w, h_s, h_b, h_len, m_h, l_h, acc_h);
+  put(2 * w + 1, c_s, c_b, c_len, m_run, l_run, acc);
+  __syncthreads();
+  // Slot headers, read once by every thread (one address for all lanes, so
+  // the values are uniform).  Slots follow the row order, and segments are
+  // disjoint and ordered, so the slots of one segment are consecutive (empty
+  // slots aside); a slot leads when no earlier slot holds its segment.
+  constexpr int NS = 2 * NW;
+  int32_t ss[NS], sn[NS];
+  int64_t sb[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    ss[i] = uni(*(const int32_t*)slot_of(i));
+    sn[i] = uni(*(const int32_t*)(slot_of(i) + 4));
+    sb[i] = uni(*(const int64_t*)(slot_of(i) + 8));
+  }
+  // Per leader: the slots of its segment (bit mask).  At most two segments
+  // cross the workgroup's range boundaries (segments are disjoint); those
+  // become partials for the last-arriver combine, the others are written.
+  uint32_t lead = 0;
+#pragma unroll
+  for (int a = 0; a < NS; ++a) {
+    bool dup = ss[a] < 0;
+#pragma unroll
+    for (int j = 0; j < a; ++j) dup = dup || ss[j] == ss[a];
+    if (!dup) lead |= 1u << a;
+  }
+  int32_t ps0 = -1, ps1 = -1, pl0 = 0, pl1 = 0;
+  int64_t pb0 = 0, pb1 = 0;
+  const int GD = G * D;
+  const int GD4 = GD / 4;
+  while (lead) {
+    const int a = __builtin_ctz(lead);
+    lead &= lead - 1;
+    int32_t sa = -1, na = 0;
+    int64_t ba = 0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+      if (j == a) {
+        sa = ss[j];
+        na = sn[j];
+        ba = sb[j];
+      }
+    uint32_t memb = 0;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) memb |= (ss[j] == sa ? 1u : 0u) << j;
+    const bool inside = ba >= B0 && ba + na <= B1;
+    const int64_t pslot = (int64_t)blockIdx.x + sa;
+    // one thread per 4 consecutive elements of one head.  Every slot is
+    // read (no branches between the loads, so they share one LDS round
+    // trip); selects drop the other segments' slots, whatever they hold.
+    for (int i4 = tid; i4 < GD4; i4 += NT) {
+      const int g = (4 * i4) / D;
+      float mv[NS], lv[NS];
+      f32x4 av[NS];
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const float* ml = (const float*)(slot_of(j) + 16);
+        mv[j] = ml[g];
+        lv[j] = ml[kMaxGroupS + g];
+        av[j] = *(const f32x4*)((const float*)(slot_of(j) + 16 + 2 * kMaxGroupS * 4) + 4 * i4);
+      }
+      float M = kNegBig;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) M = fmaxf(M, ((memb >> j) & 1) ? mv[j] : kNegBig);
+      float L = 0.f;
+      f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const bool in = (memb >> j) & 1;
+        const float sc = in ? exp2f(mv[j] - M) : 0.f;
+        L += in ? lv[j] * sc : 0.f;
+        A += in ? av[j] * sc : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      const bool lead_elem = (4 * i4) % D == 0;
+      if (inside) {
+        const float inv = 1.f / L;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const uint32_t w0 = Ops::from_f32(A[0] * inv) | (Ops::from_f32(A[1] * inv) << 16);
+        const uint32_t w1 = Ops::from_f32(A[2] * inv) | (Ops::from_f32(A[3] * inv) << 16);
+        *((WNW_GLOBAL u32x2*)gptr_w<uint16_t>(p.out) + ((int64_t)sa * GD4 + i4)) = u32x2{w0, w1};
+        if (p.lse && lead_elem) {
+          gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2] = M;
+          gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2 + 1] = L;
+        }
+      } else {
+        st_agent2(p.part_acc + pslot * GD + 4 * i4, A[0], A[1]);
+        st_agent2(p.part_acc + pslot * GD + 4 * i4 + 2, A[2], A[3]);
+        if (lead_elem) st_agent2(p.part_ml + (pslot * G + g) * 2, M, L);
+      }
+    }
+    if (!inside) {
+      if (ps0 < 0) {
+        ps0 = sa;
+        pb0 = ba;
+        pl0 = na;
+      } else {
+        ps1 = sa;
+        pb1 = ba;
+        pl1 = na;
+      }
+    }
+  }
+  wait_vmem();
+  __syncthreads();  // partials complete; the slots may be overwritten below
+  // both arrivals at once; each segment whose last partial this is merges
+  if (tid == 0) {
+    const int f0 = ps0 >= 0 && arrive(p, sl, pb0, pl0, ps0);
+    const int f1 = ps1 >= 0 && arrive(p, sl, pb1, pl1, ps1);
+    sl.is_last = f0 | (f1 << 1);
+  }
+  __syncthreads();
+  // the segments this workgroup completes are merged side by side (one
+  // half of the workgroup each when there are two)
+  const int last = uni(sl.is_last);
+  if (last) {
+    const bool both = last == 3;
+    const int nt = both ? NT / 2 : NT;
+    const bool k = both ? tid >= NT / 2 : last == 2;  // uniform per wave
+    combine_segment<T>(p, D, sl, k ? pb1 : pb0, k ? pl1 : pl0, k ? ps1 : ps0, both && k ? tid - NT / 2 : tid, nt);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -794,7 +1338,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_valu_kernel(AttnParams p) {
       }
     }
     __syncthreads();
-    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc, lds, ValuLds<D, NW>::kBytes);
+    finish_piece<T, NT, NW>(p, D, sl, pc, s, mrg_ml, mrg_acc);
   }
 }
 
@@ -848,8 +1392,32 @@ __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
     p[i] = 0u;
 }
 
+// Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
+// stream_lds_bytes (above 64 KB, so the limit is raised once per instance).
+template <typename T, int D, int QD>
+static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+  const int qslot = (ap.G * D * 2 + 255) & ~255;
+  const int lds = stream_lds_bytes(D, kNW, qslot);
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    attr_err = hipFuncSetAttribute((const void*)&attn_stream_kernel<T, D, kNW, QD>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes(D, kNW, 2048));
+  });
+  if (attr_err != hipSuccess) return attr_err;
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap);
+  return hipGetLastError();
+}
+
 template <typename T, int D>
 static hipError_t launch_attn(int kernel, const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+  if (kernel == WNW_ATTN_STREAM) {
+    if constexpr (sizeof(T) == 2 && (D == 64 || D == 128)) {
+      const int qd = (ap.G * D * 2 + 1023) / 1024;
+      if (ap.G <= kMaxGroupS) return qd == 1 ? launch_stream<T, D, 1>(ap, n_wg, st) : launch_stream<T, D, 2>(ap, n_wg, st);
+    }
+    return hipErrorInvalidValue;
+  }
   if (kernel == WNW_ATTN_MFMA) {
     if constexpr (sizeof(T) == 2 && (D == 64 || D == 128)) {
       hipLaunchKernelGGL((attn_mfma_kernel<T, D, kNW>), dim3((unsigned)n_wg), dim3(kNW * 64), 0, st, ap);
@@ -917,18 +1485,26 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                 (long long)workspace_bytes, (long long)L.total);
   int kern = kernel;
   if (kern == WNW_ATTN_AUTO)
-    kern = (dtype != WNW_F32 && (head_dim == 64 || head_dim == 128)) ? WNW_ATTN_MFMA : WNW_ATTN_VALU;
-  WNW_CHECK_ARG(kern == WNW_ATTN_MFMA || kern == WNW_ATTN_VALU, "bad kernel id %d", kernel);
+    kern = (dtype != WNW_F32 && (head_dim == 64 || head_dim == 128))
+               ? (group <= kMaxGroupS ? WNW_ATTN_STREAM : WNW_ATTN_MFMA)
+               : WNW_ATTN_VALU;
+  WNW_CHECK_ARG(kern == WNW_ATTN_MFMA || kern == WNW_ATTN_VALU || kern == WNW_ATTN_STREAM, "bad kernel id %d",
+                kernel);
+  if (kern == WNW_ATTN_STREAM)
+    WNW_CHECK_ARG(dtype != WNW_F32 && (head_dim == 64 || head_dim == 128) && group <= kMaxGroupS,
+                  "the streaming kernel needs bf16/f16, head_dim 64 or 128 and group <= %d", kMaxGroupS);
   if (kern == WNW_ATTN_MFMA)
     WNW_CHECK_ARG(dtype != WNW_F32 && (head_dim == 64 || head_dim == 128),
                   "the MFMA kernel needs bf16/f16 and head_dim 64 or 128");
   const DeviceInfo& di = device_info();
   int64_t P = n_wg;
   if (P <= 0) {
-    // Balanced split of the rows over up to 2 workgroups per CU, never
-    // fewer than ~64 rows per workgroup.
+    // Balanced split of the rows, never fewer than ~64 rows per workgroup:
+    // one workgroup per CU for the streaming kernel (its four waves keep
+    // enough loads in flight, and fewer workgroups mean fewer partials to
+    // merge), two per CU for the others.
     const int64_t by_rows = std::max<int64_t>(1, (kv_rows + 63) / 64);
-    P = std::min<int64_t>((int64_t)di.cus * 2, by_rows);
+    P = std::min<int64_t>((int64_t)di.cus * (kern == WNW_ATTN_STREAM ? 1 : 2), by_rows);
   }
   P = std::max<int64_t>(1, std::min<int64_t>(P, di.max_wg));
 

@@ -141,4 +141,21 @@ __device__ __forceinline__ WNW_GLOBAL T* gptr_w(void* p) {
   return (WNW_GLOBAL T*)p;
 }
 
+// Element i of a T array at `base` = x (rounded to nearest even), through a
+// global pointer.
+template <typename T>
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float x);
+template <>
+__device__ __forceinline__ void store_elem<float>(void* base, int64_t i, float x) {
+  gptr_w<float>(base)[i] = x;
+}
+template <>
+__device__ __forceinline__ void store_elem<bf16_t>(void* base, int64_t i, float x) {
+  gptr_w<uint16_t>(base)[i] = (uint16_t)f32_to_bf16_bits(x);
+}
+template <>
+__device__ __forceinline__ void store_elem<f16_t>(void* base, int64_t i, float x) {
+  gptr_w<uint16_t>(base)[i] = (uint16_t)f32_to_f16_bits(x);
+}
+
 }  // namespace wnw

@@ -62,7 +62,8 @@ def workspace_for(device: torch.device) -> AttnWorkspace:
     return ws
 
 
-_KERNELS = {"auto": _lib.ATTN_AUTO, "mfma": _lib.ATTN_MFMA, "valu": _lib.ATTN_VALU}
+_KERNELS = {"auto": _lib.ATTN_AUTO, "mfma": _lib.ATTN_MFMA, "valu": _lib.ATTN_VALU,
+            "stream": _lib.ATTN_STREAM}
 
 
 def decode_attn(
