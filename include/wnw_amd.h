@@ -179,8 +179,9 @@ int wnw_compact_segments(const void* src_k, const void* src_v, void* dst_k,
  * arrival counters; it must be cleared once with wnw_workspace_init before
  * its first use and may then be reused by any number of launches on one
  * stream (every launch leaves the counters at zero).  The counters occupy the
- * first 4 * n_seg bytes (rounded up to 256): before reusing a workspace for a
- * larger n_seg than it was cleared for, clear it again.
+ * first 4 * n_seg bytes (rounded up to 256) and the partials follow them, so
+ * a launch with another n_seg turns partial bytes into counters and the
+ * reverse: clear the workspace again whenever n_seg changes.
  */
 int64_t wnw_decode_attn_workspace_bytes(int64_t n_seg, int64_t group,
                                         int64_t head_dim);
@@ -232,7 +233,7 @@ int wnw_decode_attn_ex(const void* q, const void* k, const void* v,
 
 /* Workspace of wnw_decode_attn_score: the attention workspace followed by
  * the per-segment softmax normalisers.  Same clearing rule as the attention
- * workspace (wnw_workspace_init once, again before a larger n_seg). */
+ * workspace (wnw_workspace_init once, again whenever n_seg changes). */
 int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group,
                                               int64_t head_dim);
 

@@ -243,3 +243,36 @@ def test_stream_step_boundaries(gpu, lens):
         got, ref = _run_case(gpu, lens, 7, 128, "bfloat16", kernel="stream", seed=len(lens) + n_wg, n_wg=n_wg)
         ok, msg = allclose_report(got, ref, ATOL, RTOL)
         assert ok, msg
+
+
+@pytest.mark.parametrize("n_seg", [63, 64, 65, 511, 512, 513])
+def test_segment_table_sizes(gpu, n_seg):
+    """Segment counts around the 64-entry blocks of the segment walk and of
+    the workgroup ring, with and without per-segment bases."""
+    rng = np.random.default_rng(n_seg)
+    lens = rng.integers(0, 40, size=n_seg)
+    base = np.zeros(n_seg, np.int64)
+    pos = 0
+    for s in range(n_seg):
+        pos += int(rng.integers(0, 5))
+        base[s] = pos
+        pos += int(lens[s])
+    for b in (None, base):
+        for n_wg in (0, 7):
+            got, ref = _run_case(gpu, lens, 4, 64, "bfloat16", kernel="stream", seed=n_seg + n_wg, base=b,
+                                 pool_rows=pos + 1 if b is not None else None, n_wg=n_wg)
+            ok, msg = allclose_report(got, ref, ATOL, RTOL)
+            assert ok, msg
+
+
+def test_workspace_reuse_across_segment_counts(gpu):
+    """One cached workspace used with a large, a small, then a middle n_seg:
+    bytes that held partials under one layout are counters under the next,
+    so the workspace is cleared whenever n_seg changes."""
+    rng = np.random.default_rng(77)
+    for n_seg in (900, 65, 511, 65, 900):
+        lens = rng.integers(0, 40, size=n_seg)
+        for kernel in ("stream", "mfma"):
+            got, ref = _run_case(gpu, lens, 4, 64, "bfloat16", kernel=kernel, seed=n_seg, n_wg=0)
+            ok, msg = allclose_report(got, ref, ATOL, RTOL)
+            assert ok, f"n_seg={n_seg} {kernel}: {msg}"

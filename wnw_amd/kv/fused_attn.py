@@ -26,7 +26,7 @@ class AttnWorkspace:
     def __init__(self, device: torch.device):
         self.device = device
         self.buf: torch.Tensor | None = None
-        self.counter_cap = 0  # n_seg whose counter region is known to be zero
+        self.cleared_for = -1  # n_seg of the layout whose counters are known to be zero
 
     def get(self, n_seg: int, group: int, head_dim: int, score: bool = False) -> tuple[torch.Tensor, int]:
         """Buffer and its size; ``score`` adds room for the softmax
@@ -39,13 +39,14 @@ class AttnWorkspace:
         if self.buf is None or self.buf.numel() < need:
             size = max(need, 1 << 20)
             self.buf = torch.empty(size, dtype=torch.uint8, device=self.device)
-            self.counter_cap = 0
-        if n_seg > self.counter_cap:
-            # counters sit at the front, sized by n_seg: a larger n_seg reaches
-            # into bytes that held partials, so the buffer is cleared again.
+            self.cleared_for = -1
+        if n_seg != self.cleared_for:
+            # counters sit at the front, sized by n_seg, and partials follow
+            # them: under another n_seg, bytes that held partials become
+            # counters (and the reverse), so the buffer is cleared again.
             _lib.check(_lib.lib().wnw_workspace_init(_lib.ptr(self.buf), self.buf.numel(),
                                                      _lib.stream_of(self.device)), "workspace init")
-            self.counter_cap = n_seg
+            self.cleared_for = n_seg
         return self.buf, self.buf.numel()
 
 
