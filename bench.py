@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg5"])
-    ap.add_argument("--kernel", default="auto", choices=["auto", "mfma", "valu"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "stream", "mfma", "valu"])
     ap.add_argument("--attn-reps", type=int, default=20, help="attention-only graph replays for the roofline")
     ap.add_argument("--cpu-sample-layers", type=int, default=0,
                     help="layers timed for the CPU baseline (0 = choose ~15 s of work)")
