@@ -20,9 +20,14 @@
 // last arriver merges the partials by log-sum-exp and writes the output (no
 // second kernel launch).
 //
-// Inside a workgroup the NW waves take 32-row (MFMA) or 64-row (VALU) steps of
-// the piece round-robin, each keeping an online-softmax state; the wave states
-// are merged through LDS at the end of the piece.
+// Three kernels implement this split.  The streaming kernel (bf16/f16, D 64 or
+// 128, G <= 8; the default there) gives each wave a quarter of its
+// workgroup's range and streams it in 16-row steps straight into LDS; only a
+// wave's first and last pieces can be shared, and they are merged through LDS
+// after the stream.  The MFMA and VALU kernels walk the workgroup's pieces in
+// order, their NW waves taking 32-row (MFMA) or 64-row (VALU) steps of each
+// piece round-robin; the wave states are merged through LDS at the end of the
+// piece.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
