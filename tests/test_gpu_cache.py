@@ -83,6 +83,7 @@ def test_decode_steps_match_simulation(variant, fused):
     cache.rec_acc, cache.rec_topk = [], []
     if variant == "wnw_fallback":
         cache.use_triton_rebuild = False
+    cache.collect_stats(1)  # a snapshot every decode step
     print(f"cache variant={variant} fused={fused}", flush=True)
     _prefill(cache, dev, gen)
     torch.cuda.synchronize()
@@ -95,6 +96,7 @@ def test_decode_steps_match_simulation(variant, fused):
     host_k, host_v = _bits(cache.cpu_restore_k), _bits(cache.cpu_restore_v)
     meta = [[[[None if m is None else op.SegMeta(m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
                for m in cache.restore_meta[l][b][h]] for h in range(H)] for b in range(B)] for l in range(L)]
+    loaded_after_prefill = [set(x) for x in cache.loaded_segments]
     o = op.PlannerOracle(L, H, B, 2, 2, cache.chunk_to_segs, [cache.config.get_layer_class_b(l) for l in range(L)],
                          meta, copy.deepcopy(cache.loaded_segments), lens)
     groups = []  # per layer: (kv, qheads)
@@ -108,6 +110,7 @@ def test_decode_steps_match_simulation(variant, fused):
     scale = D ** -0.5
     plan = None
     n_plans = 0
+    want_events = [[] for _ in range(B)]  # (step, c2g_tokens) of the decode-time loads
     for t in range(STEPS):
         qs = [torch.randn(B, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
         ks = [torch.randn(B, H, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
@@ -120,6 +123,12 @@ def test_decode_steps_match_simulation(variant, fused):
             o.seq_lens = [list(x) for x in lens]
             plan = o.step(cache.rec_topk[t - 1])
             n_plans += int(plan.any_change)
+            for b in range(B):
+                n = sum(plan.load_lens[l][f] for l in range(L) for f in range(b * H, (b + 1) * H)) \
+                    if plan.any_change else 0
+                if n:
+                    want_events[b].append((t + 1, n))  # planned at step t, flushed with step t + 1
+            loaded_at_snapshot = [set(x) for x in o.loaded]
         acc = np.zeros(int(offs[-1]))
         for l in range(L):
             nk = _bits(ks[l].reshape(B * H, D))
@@ -158,9 +167,34 @@ def test_decode_steps_match_simulation(variant, fused):
                                       dtype=oracle.DT_BF16)
         ok, msg = allclose_report(cache.rec_acc[t], acc, 1e-6, 1e-3)
         assert ok, f"scores step {t}: {msg}"
+    # the stats record (reference cache.py:1013-1081 and inference_stats.py):
+    # the last snapshot is taken before the last step's plan
+    stats = cache.get_all_stats()
+    row = D * 2 * 2  # K and V, bf16
+    host = [{(l, h, si): m.cpu_end - m.cpu_start for l in range(L) for h in cache.config.get_layer_class_b(l)
+             for si, m in enumerate(meta[l][b][h]) if m is not None} for b in range(B)]
+    for b in range(B):
+        fin = stats[b]["decode_final"]
+        assert len(stats[b]["decode_snapshots"]) == STEPS and fin["step"] == STEPS
+        assert fin["gpu_total_tokens"] == sum(lens[l][b * H + h] for l in range(L) for h in range(H))
+        assert fin["cpu_total_tokens"] == sum(sum(x.values()) for x in host) == host_k.shape[0]
+        assert fin["cpu_restore_tokens"] == sum(host[b].values())
+        assert fin["cpu_loaded_tokens"] == sum(n for (l, h, si), n in host[b].items() if si in loaded_at_snapshot[b])
+        assert fin["memory_used_bytes"] > 0
+        events = stats[b]["cpu_gpu_events"]
+        offloaded = sum(host[b].values())
+        first_loads = sum(n for (l, h, si), n in host[b].items() if si in loaded_after_prefill[b])
+        assert events[0] == (-1, first_loads, offloaded, first_loads * row, offloaded * row), "prefill event"
+        got = [(e[0], e[1]) for e in events[1:]]
+        if variant == "wnw_cpp":
+            assert got == [], "the deferred-plan variant counts no decode loads (as the reference's)"
+        else:
+            assert got == want_events[b]
+            assert all(e[3] == e[1] * row and e[2] == 0 for e in events[1:])
     if variant != "wnw_cpp":  # the deferred variant plans at the next step's start
         o.seq_lens = [list(x) for x in lens]
         o.step(cache.rec_topk[STEPS - 1])
     for b in range(B):
         assert set(cache._planner.get_loaded_segments(b)) == o.loaded[b]
     assert n_plans > 0, "no compaction happened: the test would be vacuous"
+    assert any(want_events), "no decode-time load happened: the stats check would be vacuous"

@@ -140,6 +140,10 @@ class WnWCache(FlatVarlenCache):
         self._decode_step = 0
         self._clear_pending_rebuild_state()
 
+    # The reference's Python-planner cache counts the host rows each plan
+    # loads (cache.py:816-820); its C++-planner variant does not.
+    _record_plan_transfers = True
+
     # ------------------------------------------------------------------ setup
     def setup_audio(self, audio_starts: Tensor, audio_ends: Tensor, attention_mask: Tensor | None = None) -> None:
         """cache.py:144-166."""
@@ -592,6 +596,13 @@ class WnWCache(FlatVarlenCache):
             self._pending_evict_ends[l] = eve[lo:hi] if hi > lo else self._empty_i32
         self._segments_changed_ranges = ranges
         dt = self.layer_k[0].dtype
+        if total > 0 and self._record_plan_transfers and self.stats.enabled:
+            # cache.py:816-820: host rows loaded per sample (K and V)
+            per_row = self.head_dim * 2 * self.cpu_restore_k.element_size()
+            lens = o["load_lens_2d"].view(self.num_layers, self.batch_size, self.num_kv_heads).sum(dim=(0, 2))
+            for b, n in enumerate(lens.tolist()):
+                if n > 0:
+                    self.stats.record_cpu_gpu_transfer(b, c2g_tokens=int(n), c2g_bytes=int(n) * per_row)
         if total > 0:
             if prev_event is not None:
                 prev_event.synchronize()  # the previous copy has left staging
@@ -648,19 +659,66 @@ class WnWCache(FlatVarlenCache):
 
     # ------------------------------------------------------------------ stats
     def _snapshot_cache_stats(self, step: int = -1) -> list[dict]:
-        """cache.py:1013-1085 (per-sample GPU/CPU token accounting)."""
+        """cache.py:1013-1081: per-sample token accounting.  Audio rows on the
+        GPU are a segment's rows minus its text rows (text before the audio,
+        text after it in the prompt, one row per decode step); retention is
+        relative to L * H * num_audio."""
         if self._planner is not None:
             self.loaded_segments = [set(self._planner.get_loaded_segments(b)) for b in range(self.batch_size)]
+        L, H = self.num_layers, self.num_kv_heads
+        cpu_total = self.cpu_restore_k.shape[0] if self.cpu_restore_k is not None else 0
+        text_per_seg = self._decode_step if self.prefilled else 0
+        prefill_len = (self._seq_lengths[0] - self._decode_step) if self._seq_lengths else 0
         out = []
         for b in range(self.batch_size):
-            gpu_total = sum(self.seq_lens[l][b * self.num_kv_heads + h] for l in range(self.num_layers)
-                            for h in range(self.num_kv_heads) if self.seq_lens[l] is not None)
-            cpu_restore = sum(m.cpu_end - m.cpu_start for l in range(self.num_layers)
-                              for h in range(self.num_kv_heads) if self.config.is_class_b(l, h)
-                              for m in self.restore_meta[l][b][h] if m is not None)
-            out.append({"step": step, "gpu_total_tokens": gpu_total, "cpu_restore_tokens": cpu_restore,
-                        "loaded_segments": sorted(self.loaded_segments[b])})
+            a0, a1 = self._audio_starts_list[b], self._audio_ends_list[b]
+            num_audio = a1 - a0
+            full_audio = L * H * num_audio
+            non_audio = a0 + max(0, max(0, prefill_len - self.pad_lens_list[b]) - a1)
+            gpu_audio = gpu_total = 0
+            per_layer = []
+            for l in range(L):
+                if self.seq_lens[l] is None:
+                    per_layer.append(0)
+                    continue
+                layer_audio = 0
+                for h in range(H):
+                    n = self.seq_lens[l][b * H + h]
+                    gpu_total += n
+                    layer_audio += max(0, n - non_audio - text_per_seg)
+                gpu_audio += layer_audio
+                per_layer.append(layer_audio)
+            metas = [(l, h) for l in range(L) for h in range(H) if self.config.is_class_b(l, h)]
+            cpu_restore = sum(m.cpu_end - m.cpu_start for l, h in metas for m in self.restore_meta[l][b][h]
+                              if m is not None) if self.restore_meta else 0
+            cpu_loaded = 0
+            if self.prefilled:
+                for si in self.loaded_segments[b]:
+                    for l, h in metas:
+                        m = self.restore_meta[l][b][h][si]
+                        if m is not None:
+                            cpu_loaded += m.cpu_end - m.cpu_start
+            out.append({
+                "step": step,
+                "num_audio": num_audio,
+                "gpu_audio_tokens": gpu_audio,
+                "gpu_total_tokens": gpu_total,
+                "audio_retention": gpu_audio / full_audio if full_audio > 0 else 1.0,
+                "per_layer_audio_tokens": per_layer,
+                "cpu_total_tokens": cpu_total,
+                "cpu_loaded_tokens": cpu_loaded,
+                "cpu_restore_tokens": cpu_restore,
+                "gpu_plus_cpu_retention": (gpu_audio + cpu_restore) / full_audio if full_audio > 0 else 1.0,
+            })
         return out
+
+    def get_snapshot_stats(self, step: int = -1) -> list[dict]:
+        """cache.py:1082-1084."""
+        return self._snapshot_cache_stats(step=step)
+
+    def get_compression_stats(self) -> list[dict]:
+        """cache.py:1086-1088."""
+        return self._snapshot_cache_stats(step=-1)
 
     def get_all_stats(self) -> list[dict]:
         return self.stats.get_all_stats()

@@ -24,6 +24,7 @@ class WnWCppCache(WnWCache):
     def __init__(self, *args, **kwargs):
         super().__init__(*args, **kwargs)
         self._fallback = os.environ.get("WNW_CPP_FALLBACK", "0") == "1"
+        self._record_plan_transfers = self._fallback  # the C++-planner flow counts no decode loads
         self._topk_pending = False
         self._topk_idx_masked = None
 
