@@ -135,8 +135,6 @@ class WnWCache(FlatVarlenCache):
         self._class_b_heads_by_layer = [config.get_layer_class_b(l) for l in range(num_layers)]
         self._transfer_stream: torch.cuda.Stream | None = None
         self._planner: Planner | None = None
-        self._staging_k: Tensor | None = None
-        self._staging_v: Tensor | None = None
         self._decode_step = 0
         self._clear_pending_rebuild_state()
 
@@ -404,11 +402,11 @@ class WnWCache(FlatVarlenCache):
         for b in range(B):
             p.set_loaded(b, sorted(self.loaded_segments[b]))
         p.set_seq_lens([x for l in range(L) for x in self.seq_lens[l]])
-        n_restore = self.cpu_restore_k.shape[0]
-        if n_restore > 0:
-            self._staging_k = torch.empty(n_restore, self.head_dim, dtype=self.cpu_restore_k.dtype, pin_memory=True)
-            self._staging_v = torch.empty(n_restore, self.head_dim, dtype=self.cpu_restore_v.dtype, pin_memory=True)
-            p.set_restore_buffers(self.cpu_restore_k, self.cpu_restore_v, self._staging_k, self._staging_v)
+        # two pinned staging pairs, used in turn and grown on demand: a plan's
+        # gather waits only for the copy that used its pair two plans ago
+        self._staging = [None, None]
+        self._staging_events: list = [None, None]
+        self._staging_turn = 0
         N = B * H
         self._plan_out = dict(
             load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
@@ -577,7 +575,6 @@ class WnWCache(FlatVarlenCache):
         device, host rows gathered into pinned staging and copied on the
         transfer stream."""
         total, ev_s, ev_e, ranges = self._plan_result
-        prev_event = self._pending_transfer_event
         self._clear_pending_rebuild_state()
         o = self._plan_out
         dev = self.device
@@ -604,19 +601,39 @@ class WnWCache(FlatVarlenCache):
                 if n > 0:
                     self.stats.record_cpu_gpu_transfer(b, c2g_tokens=int(n), c2g_bytes=int(n) * per_row)
         if total > 0:
-            if prev_event is not None:
-                prev_event.synchronize()  # the previous copy has left staging
+            stg_k, stg_v = self._staging_pair(total)
             self._planner.gather_restore()
             stream = self._get_transfer_stream()
             ev = torch.cuda.Event()
             with torch.cuda.stream(stream):
-                self._pending_gpu_k = self._staging_k[:total].to(dev, non_blocking=True)
-                self._pending_gpu_v = self._staging_v[:total].to(dev, non_blocking=True)
+                self._pending_gpu_k = stg_k[:total].to(dev, non_blocking=True)
+                self._pending_gpu_v = stg_v[:total].to(dev, non_blocking=True)
                 ev.record(stream)
             self._pending_transfer_event = ev
+            self._staging_events[self._staging_turn ^ 1] = ev
         else:
             self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
             self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
+
+    def _staging_pair(self, rows: int) -> tuple[Tensor, Tensor]:
+        """The next staging pair, holding at least `rows` rows, handed to the
+        planner.  Its previous copy (two plans ago) must have left it; the
+        pair grows to the next power of two (cache.py:128-134 grows its one
+        staging buffer the same way)."""
+        i = self._staging_turn
+        self._staging_turn ^= 1
+        if self._staging_events[i] is not None:
+            self._staging_events[i].synchronize()
+            self._staging_events[i] = None
+        pair = self._staging[i]
+        if pair is None or pair[0].shape[0] < rows:
+            cap = min(1 << max(0, rows - 1).bit_length(), max(rows, self.cpu_restore_k.shape[0]))
+            dt = self.cpu_restore_k.dtype
+            pair = (torch.empty(cap, self.head_dim, dtype=dt, pin_memory=True),
+                    torch.empty(cap, self.head_dim, dtype=dt, pin_memory=True))
+            self._staging[i] = pair
+        self._planner.set_restore_buffers(self.cpu_restore_k, self.cpu_restore_v, pair[0], pair[1])
+        return pair
 
     def _rebuild_append_layer(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
         """cache.py:716-754: compaction + load + append in one launch."""
