@@ -47,7 +47,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg5"])
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"],
+                    help="cfg4 runs whole decode steps through the cache with host->device chunk fetches")
     ap.add_argument("--kernel", default="auto", choices=["auto", "stream", "mfma", "valu"])
     ap.add_argument("--attn-reps", type=int, default=20, help="attention-only graph replays for the roofline")
     ap.add_argument("--cpu-sample-layers", type=int, default=0,
@@ -118,6 +119,11 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.config == "cfg4":
+        from wnw_amd import offload_bench
+
+        print(json.dumps({**offload_bench.run(args.steps, args.warmup), "n_gpus": 1}), flush=True)
         return
 
     import numpy as np

@@ -363,6 +363,31 @@ int wnw_planner_get_evictions(wnw_planner* p, int32_t* starts, int32_t* ends,
 /* The `ranges` [n, 2] tensor of compute_and_prepare's result tuple */
 int wnw_planner_get_ranges(wnw_planner* p, int32_t* ranges, int64_t cap);
 
+/* Offload channel                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* 1 if the device can read both host arrays directly (pinned, mapped host
+ * memory), else 0. */
+int wnw_host_rows_readable(const void* host_k, const void* host_v);
+
+/*
+ * Device-side gather of planned host rows, in place of the host gather into
+ * staging plus the staging copy (planner.cpp:113-122 with
+ * wnw_cpp/code/cache.py:287-295; cache.py:868-881 in the Python planner).
+ * For r in [r0, r1): rows [ranges[2r], ranges[2r+1]) of host_k / host_v
+ * (pinned, host_rows rows of row_bytes) go to rows [dst_off[r],
+ * dst_off[r+1]) of out_k / out_v (device, out_rows rows).  ranges (int32
+ * [n, 2], the planner's transfer order) and dst_off (int64 [n + 1], prefix
+ * sums of the range lengths) are device arrays.  Asynchronous on `stream`;
+ * a range outside either array sets WNW_DEVERR_BOUNDS and is skipped.
+ * Returns WNW_ENOTSUP when the device cannot read the host arrays.
+ */
+int wnw_gather_host_rows(const void* host_k, const void* host_v,
+                         int64_t host_rows, const int32_t* ranges,
+                         const int64_t* dst_off, int64_t r0, int64_t r1,
+                         int64_t row_bytes, void* out_k, void* out_v,
+                         int64_t out_rows, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

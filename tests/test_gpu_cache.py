@@ -72,10 +72,13 @@ def _prefill(cache, dev, gen):
     cache.prefill_all_layers_done()
 
 
-@pytest.mark.parametrize("variant,fused", [("wnw", True), ("wnw", False), ("wnw_fallback", True),
-                                           ("wnw_cpp", True)])
-def test_decode_steps_match_simulation(variant, fused):
+@pytest.mark.parametrize("variant,fused,host_gather", [("wnw", True, False), ("wnw", False, False),
+                                                       ("wnw_fallback", True, False), ("wnw_cpp", True, False),
+                                                       ("wnw", True, True), ("wnw_cpp", True, True)])
+def test_decode_steps_match_simulation(variant, fused, host_gather, monkeypatch):
     dev = torch.device("cuda", 0)
+    if host_gather:  # loads through the host gather + staging copy instead of the device gather
+        monkeypatch.setenv("WNW_HOST_GATHER", "1")
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     cls = _recording(WnWCppCache if variant == "wnw_cpp" else WnWCache)
@@ -84,10 +87,11 @@ def test_decode_steps_match_simulation(variant, fused):
     if variant == "wnw_fallback":
         cache.use_triton_rebuild = False
     cache.collect_stats(1)  # a snapshot every decode step
-    print(f"cache variant={variant} fused={fused}", flush=True)
+    print(f"cache variant={variant} fused={fused} host_gather={host_gather}", flush=True)
     _prefill(cache, dev, gen)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
+    assert cache._device_gather == (not host_gather)
 
     # simulation state, taken from the prefilled cache
     K = [_bits(cache.layer_k[l]) for l in range(L)]

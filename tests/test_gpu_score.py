@@ -130,3 +130,42 @@ def test_score_bad_audio_range_is_flagged():
     assert _lib.device_error() & _lib.DEVERR_BOUNDS
     assert float(acc[:50].abs().sum()) == 0.0  # the bad item wrote nothing
     assert _lib.device_error() == 0
+
+
+def test_attn_score_many_samples():
+    """Enough samples x audio rows for the long (16-iteration) scoring workgroups."""
+    rng = np.random.default_rng(12)
+    B, H = 24, 2
+    lens = [int(x) for x in rng.integers(6000, 6100, size=B * H)]
+    a_s, a_e = [0] * B, [6000] * B
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, 4, 128, [1, 0], a_s, a_e, seed=12)
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+def test_fused_score_accumulate_many_samples():
+    """fused_score_accumulate with the long (16-iteration) scoring workgroups."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(13)
+    S, nh, D = 24, 2, 128
+    lens = rng.integers(6000, 6100, size=S)
+    starts = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    ends = starts + lens
+    k = rand_rows(rng, int(ends[-1]), D, "bfloat16")
+    q = rand_rows(rng, S * nh, D, "bfloat16").reshape(S, nh, D)
+    a_s = np.zeros(S, np.int32)
+    a_e = np.full(S, 6000, np.int32)
+    offs = np.concatenate([[0], np.cumsum(a_e - a_s)]).astype(np.int32)
+    acc0 = rng.random(int(offs[-1])).astype(np.float32)
+    ref = oracle.segment_scores(q, k, starts, ends, a_s, a_e, offs[:-1], D ** -0.5, acc0.astype(np.float64),
+                                dtype=oracle.DT_BF16)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(dev)  # noqa: E731
+    acc = torch.from_numpy(acc0).to(dev)
+    wk.fused_score_accumulate(to_torch(q, "bfloat16", dev), to_torch(k, "bfloat16", dev), t(starts), t(ends),
+                              t(a_s), t(a_e), acc, t(offs))
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    ok, msg = allclose_report(acc.cpu().numpy().astype(np.float64), ref, S_ATOL, S_RTOL)
+    assert ok, msg

@@ -59,6 +59,8 @@ _SIGNATURES = {
     "wnw_planner_get_loaded_segments": (_i64, [_vp, _i32, _vp, _i64]),
     "wnw_planner_set_restore_buffers": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64]),
     "wnw_planner_gather_restore": (_i32, [_vp]),
+    "wnw_host_rows_readable": (_i32, [_vp, _vp]),
+    "wnw_gather_host_rows": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "wnw_planner_compute_and_prepare": (_i32, [_vp] * 14),
     "wnw_planner_get_evictions": (_i32, [_vp, _vp, _vp, _i64]),
     "wnw_planner_get_ranges": (_i32, [_vp, _vp, _i64]),

@@ -35,7 +35,10 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                      void* stream);
 
 static constexpr int kScoreThreads = 256;
-static constexpr int kIters = 16;         // row iterations per scoring workgroup
+// Row iterations per scoring workgroup: 16, or 4 when 16 would leave CUs idle
+// (few samples or short audio).
+static constexpr int kIters = 16;
+static constexpr int kItersSmall = 4;
 static constexpr int kStatChunks = 32;    // row slices per segment in the statistics pass
 static constexpr int kMaxHeads = 16;
 static constexpr float kLog2eS = 1.4426950408889634f;
@@ -45,10 +48,10 @@ template <typename T>
 struct RowGeom {
   static constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
 };
-// Rows one scoring workgroup covers: kIters iterations of kScoreThreads / LPR
+// Rows one scoring workgroup covers: `iters` iterations of kScoreThreads / LPR
 // rows, LPR = head_dim / EPC lanes per row.
-__host__ __device__ constexpr int score_rows_per_wg(int head_dim, int elem_bytes) {
-  return kIters * kScoreThreads / (head_dim / (16 / elem_bytes));
+__host__ __device__ constexpr int score_rows_per_wg(int head_dim, int elem_bytes, int iters = kIters) {
+  return iters * kScoreThreads / (head_dim / (16 / elem_bytes));
 }
 
 // 16-byte chunk -> EPC floats
@@ -96,7 +99,7 @@ struct AttnScoreParams {
   float scale_log2;
 };
 
-template <typename T, int D>
+template <typename T, int D, int IT>
 __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScoreParams p) {
   constexpr int EPC = RowGeom<T>::EPC;
   constexpr int LPR = D / EPC;            // lanes per row
@@ -109,12 +112,12 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
   const int rl = tid / LPR;               // row slot in an iteration
   const int a0 = p.audio_s[b], a1 = p.audio_e[b];
   const int n_audio = a1 - a0;
-  const int j0 = blockIdx.x * RPI * kIters;
+  const int j0 = blockIdx.x * RPI * IT;
   if (j0 >= n_audio) return;  // workgroup-uniform
   const int64_t off = p.acc_off[b];
-  float total[kIters];
+  float total[IT];
 #pragma unroll
-  for (int i = 0; i < kIters; ++i) total[i] = 0.f;
+  for (int i = 0; i < IT; ++i) total[i] = 0.f;
   const T* kp = (const T*)p.k;
   for (int kv = 0; kv < p.Hkv; ++kv) {
     if (!p.mask[kv]) continue;
@@ -134,7 +137,7 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
     }
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < kIters; ++it) {
+    for (int it = 0; it < IT; ++it) {
       const int j = j0 + it * RPI + rl;
       const bool valid = j < n_audio;
       const int64_t row = base + a0 + (valid ? j : 0);
@@ -154,7 +157,7 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
   }
   if (sub == 0) {
 #pragma unroll
-    for (int it = 0; it < kIters; ++it) {
+    for (int it = 0; it < IT; ++it) {
       const int j = j0 + it * RPI + rl;
       if (j < n_audio) p.acc[off + j] += total[it];
     }
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(kScoreThreads) void seg_stats_kernel(SegScoreParams
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int IT>
 __global__ __launch_bounds__(kScoreThreads) void seg_score_kernel(SegScoreParams p) {
   constexpr int EPC = RowGeom<T>::EPC;
   constexpr int LPR = D / EPC;
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(kScoreThreads) void seg_score_kernel(SegScoreParams
   const int64_t r0 = p.seg_s[s], r1 = p.seg_e[s];
   const int a0 = p.audio_s[s], a1 = p.audio_e[s];
   const int n_audio = a1 - a0;
-  const int j0 = blockIdx.x * RPI * kIters;
+  const int j0 = blockIdx.x * RPI * IT;
   if (j0 >= n_audio) return;
   const int64_t off = p.acc_off[s];
   if (r0 < 0 || r1 < r0 || r1 > p.k_rows || a0 < 0 || r0 + a1 > r1 || off + n_audio > p.acc_len) {
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(kScoreThreads) void seg_score_kernel(SegScoreParams
   }
   __syncthreads();
   const T* kp = (const T*)p.k;
-  for (int it = 0; it < kIters; ++it) {
+  for (int it = 0; it < IT; ++it) {
     const int j = j0 + it * RPI + rl;
     const bool valid = j < n_audio;
     const int64_t row = r0 + a0 + (valid ? j : 0);
@@ -309,32 +312,52 @@ __global__ __launch_bounds__(kScoreThreads) void seg_score_kernel(SegScoreParams
 enum ScoreKernel { kAttnScore = 0, kSegStats = 1, kSegScore = 2 };
 
 template <typename T, int D>
-static const void* score_fn(int which) {
+static const void* score_fn(int which, int iters) {
+  const bool small = iters == kItersSmall;
   switch (which) {
-    case kAttnScore: return (const void*)&attn_score_kernel<T, D>;
+    case kAttnScore:
+      return small ? (const void*)&attn_score_kernel<T, D, kItersSmall> : (const void*)&attn_score_kernel<T, D, kIters>;
     case kSegStats: return (const void*)&seg_stats_kernel<T, D>;
-    case kSegScore: return (const void*)&seg_score_kernel<T, D>;
+    case kSegScore:
+      return small ? (const void*)&seg_score_kernel<T, D, kItersSmall> : (const void*)&seg_score_kernel<T, D, kIters>;
   }
   return nullptr;
 }
 
 template <typename T>
-static const void* score_fn_d(int which, int64_t D) {
+static const void* score_fn_d(int which, int64_t D, int iters) {
   switch (D) {
-    case 64: return score_fn<T, 64>(which);
-    case 128: return score_fn<T, 128>(which);
-    case 256: return score_fn<T, 256>(which);
+    case 64: return score_fn<T, 64>(which, iters);
+    case 128: return score_fn<T, 128>(which, iters);
+    case 256: return score_fn<T, 256>(which, iters);
   }
   return nullptr;
 }
 
+// Rows per iteration count for a scoring grid of `ny` rows of workgroups over
+// max_audio rows: 16 iterations when that still gives two workgroups per CU,
+// else 4 (more, shorter workgroups).
+static int score_iters(int64_t max_audio, int64_t ny, int64_t head_dim, int elem_bytes) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                                                 hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  const int64_t rows16 = score_rows_per_wg((int)head_dim, elem_bytes, kIters);
+  return ((max_audio + rows16 - 1) / rows16) * ny >= 2 * (int64_t)cus ? kIters : kItersSmall;
+}
+
 template <typename P>
-static hipError_t launch_score(int which, int dtype, int64_t D, dim3 grid, P prm, hipStream_t st) {
+static hipError_t launch_score(int which, int dtype, int64_t D, int iters, dim3 grid, P prm, hipStream_t st) {
   const void* fn = nullptr;
   switch (dtype) {
-    case WNW_BF16: fn = score_fn_d<bf16_t>(which, D); break;
-    case WNW_F16: fn = score_fn_d<f16_t>(which, D); break;
-    case WNW_F32: fn = score_fn_d<float>(which, D); break;
+    case WNW_BF16: fn = score_fn_d<bf16_t>(which, D, iters); break;
+    case WNW_F16: fn = score_fn_d<f16_t>(which, D, iters); break;
+    case WNW_F32: fn = score_fn_d<float>(which, D, iters); break;
   }
   if (!fn) return hipErrorInvalidValue;
   void* args[] = {&prm};
@@ -392,9 +415,10 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   sp.G = (int32_t)group;
   sp.Hkv = (int32_t)num_kv_heads;
   sp.scale_log2 = scale * kLog2eS;
-  const int rows_wg = score_rows_per_wg((int)head_dim, elem_bytes(dtype));
+  const int iters = score_iters(max_audio, n_seg / num_kv_heads, head_dim, elem_bytes(dtype));
+  const int rows_wg = score_rows_per_wg((int)head_dim, elem_bytes(dtype), iters);
   const dim3 grid((unsigned)((max_audio + rows_wg - 1) / rows_wg), (unsigned)(n_seg / num_kv_heads));
-  WNW_CHECK_HIP(launch_score(kAttnScore, dtype, head_dim, grid, sp, (hipStream_t)stream),
+  WNW_CHECK_HIP(launch_score(kAttnScore, dtype, head_dim, iters, grid, sp, (hipStream_t)stream),
                 "attention score launch");
   return WNW_OK;
 }
@@ -439,10 +463,11 @@ extern "C" int wnw_fused_score_accumulate(const void* q, const void* k, const in
   sp.nh = (int32_t)n_heads;
   sp.scale_log2 = scale * kLog2eS;
   hipStream_t st = (hipStream_t)stream;
-  WNW_CHECK_HIP(launch_score(kSegStats, dtype, head_dim, dim3(kStatChunks, (unsigned)n_samples), sp, st),
+  WNW_CHECK_HIP(launch_score(kSegStats, dtype, head_dim, kIters, dim3(kStatChunks, (unsigned)n_samples), sp, st),
                 "score statistics launch");
-  const int rows_wg = score_rows_per_wg((int)head_dim, elem_bytes(dtype));
+  const int iters = score_iters(max_audio, n_samples, head_dim, elem_bytes(dtype));
+  const int rows_wg = score_rows_per_wg((int)head_dim, elem_bytes(dtype), iters);
   const dim3 grid((unsigned)((max_audio + rows_wg - 1) / rows_wg), (unsigned)n_samples);
-  WNW_CHECK_HIP(launch_score(kSegScore, dtype, head_dim, grid, sp, st), "score launch");
+  WNW_CHECK_HIP(launch_score(kSegScore, dtype, head_dim, iters, grid, sp, st), "score launch");
   return WNW_OK;
 }

@@ -46,7 +46,7 @@ from ..kv.fused_attn import q1_decode_attn, q1_decode_attn_score
 from ..kv.kernels import interleave_append
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
-from .kernels import fused_score_accumulate, rebuild_append_kv
+from .kernels import fused_score_accumulate, gather_host_rows, host_rows_readable, rebuild_append_kv
 
 
 @dataclass
@@ -195,8 +195,7 @@ class WnWCache(FlatVarlenCache):
 
     def _clear_pending_rebuild_state(self) -> None:
         L = self.num_layers
-        self._pending_transfer_event: torch.cuda.Event | None = None
-        self._pending_transfer_waited = False
+        self._pending_layer_events: list = [None] * L  # per layer: the copy of its loaded rows
         self._pending_gpu_k: Tensor | None = None
         self._pending_gpu_v: Tensor | None = None
         self._pending_load_starts: list = [None] * L
@@ -407,6 +406,11 @@ class WnWCache(FlatVarlenCache):
         self._staging = [None, None]
         self._staging_events: list = [None, None]
         self._staging_turn = 0
+        # the device reads the pinned restore rows itself unless they are not
+        # readable or WNW_HOST_GATHER=1 asks for the host gather + staging copy
+        self._gather_launches = 6  # launches (events) per plan: copy/compute overlap vs launch cost
+        self._device_gather = os.environ.get("WNW_HOST_GATHER", "0") != "1" and \
+            self.cpu_restore_k.shape[0] > 0 and host_rows_readable(self.cpu_restore_k, self.cpu_restore_v)
         N = B * H
         self._plan_out = dict(
             load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
@@ -600,7 +604,9 @@ class WnWCache(FlatVarlenCache):
             for b, n in enumerate(lens.tolist()):
                 if n > 0:
                     self.stats.record_cpu_gpu_transfer(b, c2g_tokens=int(n), c2g_bytes=int(n) * per_row)
-        if total > 0:
+        if total > 0 and self._device_gather:
+            self._gather_loads_on_device(total, ranges, o["load_lens_2d"])
+        elif total > 0:
             stg_k, stg_v = self._staging_pair(total)
             self._planner.gather_restore()
             stream = self._get_transfer_stream()
@@ -609,11 +615,51 @@ class WnWCache(FlatVarlenCache):
                 self._pending_gpu_k = stg_k[:total].to(dev, non_blocking=True)
                 self._pending_gpu_v = stg_v[:total].to(dev, non_blocking=True)
                 ev.record(stream)
-            self._pending_transfer_event = ev
+            compute = torch.cuda.current_stream(dev)
+            self._pending_gpu_k.record_stream(compute)
+            self._pending_gpu_v.record_stream(compute)
+            self._pending_layer_events = [ev] * self.num_layers
             self._staging_events[self._staging_turn ^ 1] = ev
         else:
             self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
             self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
+
+    def _gather_loads_on_device(self, total: int, ranges: Tensor, load_lens_2d: Tensor) -> None:
+        """The plan's host ranges read by the device straight from the pinned
+        restore arrays (no host gather, no staging), on the transfer stream in
+        a few launches of consecutive layers with an event each: a layer's
+        rebuild waits only for its own launch, so later layers' copies overlap
+        earlier layers' compute.  Ranges are in transfer order (layer, sample,
+        head, segment), so each layer's rows and ranges are contiguous."""
+        dev = self.device
+        lens = (ranges[:, 1] - ranges[:, 0]).to(torch.int64)
+        dst = torch.zeros(ranges.shape[0] + 1, dtype=torch.int64)
+        torch.cumsum(lens, 0, out=dst[1:])
+        layer_rows = load_lens_2d.to(torch.int64).sum(dim=1)
+        bounds = torch.searchsorted(dst, torch.cumsum(layer_rows, 0)).tolist()
+        compute = torch.cuda.current_stream(dev)
+        stream = self._get_transfer_stream()
+        events = [None] * self.num_layers
+        per_launch = max(1, -(-self.num_layers // self._gather_launches))
+        with torch.cuda.stream(stream):
+            rg = ranges.to(dev)
+            do = dst.to(dev)
+            pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
+            pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
+            r0 = 0
+            for l0 in range(0, self.num_layers, per_launch):
+                l1 = min(l0 + per_launch, self.num_layers)
+                r1 = bounds[l1 - 1]
+                if r1 > r0:
+                    gather_host_rows(self.cpu_restore_k, self.cpu_restore_v, rg, do, r0, r1, pk, pv)
+                    ev = torch.cuda.Event()
+                    ev.record(stream)
+                    events[l0:l1] = [ev] * (l1 - l0)
+                r0 = r1
+        for t in (pk, pv, rg, do):
+            t.record_stream(compute)
+        self._pending_gpu_k, self._pending_gpu_v = pk, pv
+        self._pending_layer_events = events
 
     def _staging_pair(self, rows: int) -> tuple[Tensor, Tensor]:
         """The next staging pair, holding at least `rows` rows, handed to the
@@ -637,9 +683,7 @@ class WnWCache(FlatVarlenCache):
 
     def _rebuild_append_layer(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
         """cache.py:716-754: compaction + load + append in one launch."""
-        if self._pending_transfer_event is not None and not self._pending_transfer_waited:
-            torch.cuda.current_stream(self.device).wait_event(self._pending_transfer_event)
-            self._pending_transfer_waited = True
+        self._wait_loads(layer_idx)
         nk = new_k.squeeze(2).reshape(-1, self.head_dim)
         nv = new_v.squeeze(2).reshape(-1, self.head_dim)
         cu_new = self._pending_cu_new[layer_idx]
@@ -656,13 +700,19 @@ class WnWCache(FlatVarlenCache):
     def _apply_chunk_update_to_layer(self, layer_idx: int) -> None:
         """cache.py:891-1010 (the fallback without the fused append): the
         same compaction and load, then the ordinary append follows."""
-        if self._pending_transfer_event is not None and not self._pending_transfer_waited:
-            torch.cuda.current_stream(self.device).wait_event(self._pending_transfer_event)
-            self._pending_transfer_waited = True
+        self._wait_loads(layer_idx)
         lens_after = [x - 1 for x in self._pending_new_lens[layer_idx]]  # the append comes next
         cu_mid = _build_cu_seqlens(lens_after, self.device)
         k, v = _compact_no_append(self, layer_idx, cu_mid, lens_after)
         self._finish_layer(layer_idx, k, v, cu_mid, lens_after)
+
+    def _wait_loads(self, layer_idx: int) -> None:
+        """The compute stream waits for the copy of this layer's loaded rows
+        (cache.py:719-721 waits once for the whole transfer)."""
+        ev = self._pending_layer_events[layer_idx]
+        if ev is not None:
+            torch.cuda.current_stream(self.device).wait_event(ev)
+            self._pending_layer_events[layer_idx] = None
 
     def _finish_layer(self, layer_idx, k, v, cu_new, new_lens) -> None:
         self.layer_k[layer_idx], self.layer_v[layer_idx] = k, v

@@ -190,3 +190,31 @@ def compact_segments(
         _lib.ptr(ee), n_ev, 1 if with_new else 0, src_k.shape[0], dst_k.shape[0],
         0 if lk is None else lk.shape[0], d, _lib.dtype_code(src_k.dtype), _lib.stream_of(src_k.device)),
         "compact_segments")
+
+
+def host_rows_readable(host_k: torch.Tensor, host_v: torch.Tensor) -> bool:
+    """Whether the device can read the two host arrays directly (pinned)."""
+    return bool(_lib.lib().wnw_host_rows_readable(_lib.ptr(host_k), _lib.ptr(host_v)))
+
+
+def gather_host_rows(host_k: torch.Tensor, host_v: torch.Tensor, ranges: torch.Tensor, dst_off: torch.Tensor,
+                     r0: int, r1: int, out_k: torch.Tensor, out_v: torch.Tensor) -> None:
+    """Rows [ranges[r, 0], ranges[r, 1]) of the pinned host arrays, for r in
+    [r0, r1), into rows [dst_off[r], dst_off[r + 1]) of out_k / out_v, on the
+    current stream (the device reads host memory itself; it replaces the
+    host gather into staging + staging copy of the reference's offload,
+    src/algorithms/wnw_cpp/code/planner.cpp:113-122 and cache.py:287-295).
+    ``ranges`` int32 [n, 2] and ``dst_off`` int64 [n + 1] live on the device."""
+    for t in (host_k, host_v):
+        if t.device.type != "cpu" or not t.is_pinned() or not t.is_contiguous() or t.dim() != 2:
+            raise _lib.WnwError("host rows must be contiguous 2-D pinned tensors")
+    if host_k.shape != host_v.shape or out_k.shape != out_v.shape or out_k.shape[1:] != host_k.shape[1:] \
+            or out_k.dtype != host_k.dtype or out_v.dtype != host_v.dtype:
+        raise _lib.WnwError("host / output shapes or dtypes differ")
+    if ranges.dtype != torch.int32 or dst_off.dtype != torch.int64 or ranges.device != out_k.device \
+            or dst_off.device != out_k.device:
+        raise _lib.WnwError("ranges must be int32 and dst_off int64, on the outputs' device")
+    row_bytes = host_k.shape[1] * host_k.element_size()
+    _lib.check(_lib.lib().wnw_gather_host_rows(
+        _lib.ptr(host_k), _lib.ptr(host_v), host_k.shape[0], _lib.ptr(ranges), _lib.ptr(dst_off), r0, r1, row_bytes,
+        _lib.ptr(out_k), _lib.ptr(out_v), out_k.shape[0], _lib.stream_of(out_k.device)), "gather_host_rows")
