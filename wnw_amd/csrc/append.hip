@@ -81,6 +81,58 @@ __device__ __forceinline__ int64_t seg_hi(const BlockSegs& bs, const int32_t* cu
   return (bs.s_last - bs.s_first < kSegRing) ? bs.out_hi[s % kSegRing] : cu_out[s + 1];
 }
 
+// Where each output row of a block comes from, resolved once per row by the
+// block's first wave (the lookups are short chains of dependent loads), so
+// that the copy loop below issues its data loads back to back.
+enum RowKind : int32_t { kOld = 0, kLoad = 1, kNew = 2, kNone = 3 };
+struct RowSrc {
+  int64_t row[kRows];   // source row in the tensor its kind names
+  int32_t kind[kRows];  // RowKind; kNone writes zeros (an error was raised)
+};
+
+// Copies the block's nrows rows: output row out_row0 + r <- row rs.row[r] of
+// (k, v)[rs.kind[r]].  Each thread has four 16-byte chunks of each tensor in
+// flight; a wave's loads and stores cover contiguous spans of the rows.
+template <bool KV>
+__device__ __forceinline__ void copy_rows(const RowSrc& rs, int nrows, int cpr, const u32x4* k0,
+                                          const u32x4* v0, const u32x4* k1, const u32x4* v1,
+                                          const u32x4* k2, const u32x4* v2, int64_t out_row0,
+                                          u32x4* out_k, u32x4* out_v) {
+  constexpr int U = 4;
+  const int n = nrows * cpr;
+  WNW_GLOBAL u32x4* ok = (WNW_GLOBAL u32x4*)out_k + out_row0 * cpr;
+  WNW_GLOBAL u32x4* ov = KV ? (WNW_GLOBAL u32x4*)out_v + out_row0 * cpr : nullptr;
+  for (int x0 = threadIdx.x; x0 < n; x0 += U * kNT) {
+    u32x4 a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int x = x0 + u * kNT;
+      a[u] = b[u] = u32x4{0, 0, 0, 0};
+      if (x < n) {
+        const int r = x / cpr;
+        const int kind = rs.kind[r];
+        if (kind != kNone) {
+          const int64_t off = rs.row[r] * cpr + (x - r * cpr);
+          const u32x4* pk = kind == kOld ? k0 : kind == kLoad ? k1 : k2;
+          a[u] = ((const WNW_GLOBAL u32x4*)pk)[off];
+          if (KV) {
+            const u32x4* pv = kind == kOld ? v0 : kind == kLoad ? v1 : v2;
+            b[u] = ((const WNW_GLOBAL u32x4*)pv)[off];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int x = x0 + u * kNT;
+      if (x < n) {
+        ok[x] = a[u];
+        if (KV) ov[x] = b[u];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // interleave_append (reference src/common/kv/kernels.py:7-73)
 // ---------------------------------------------------------------------------
@@ -89,14 +141,15 @@ __global__ __launch_bounds__(kNT) void interleave_append_kernel(
     const int32_t* __restrict__ cu_old, const int32_t* __restrict__ cu_new, int N,
     int64_t total_old, int64_t total_out, int cpr, u32x4* __restrict__ out, int32_t* err) {
   __shared__ BlockSegs bs;
+  __shared__ RowSrc rs;
   const int64_t B0 = (int64_t)blockIdx.x * kRows;
   const int64_t B1 = min(B0 + kRows, total_out);
+  const int nrows = (int)(B1 - B0);
   scan_block_segments(cu_new, N, B0, B1, bs, err);
-  const int64_t nchunks = (B1 - B0) * cpr;
-  for (int64_t x = threadIdx.x; x < nchunks; x += kNT) {
-    const int64_t j = B0 + x / cpr;
-    const int c = (int)(x % cpr);
-    u32x4 val = u32x4{0, 0, 0, 0};
+  if ((int)threadIdx.x < nrows) {
+    const int64_t j = B0 + threadIdx.x;
+    int kind = kNone;
+    int64_t src = 0;
     if (bs.s_first > bs.s_last || j >= seg_hi(bs, cu_new, bs.s_last) || j < seg_lo(bs, cu_new, bs.s_first)) {
       raise_device_error(err, WNW_DEVERR_BOUNDS);  // row not covered by cu_new
     } else {
@@ -104,17 +157,21 @@ __global__ __launch_bounds__(kNT) void interleave_append_kernel(
       const int64_t i = j - seg_lo(bs, cu_new, s);
       const int64_t olo = cu_old[s], ohi = cu_old[s + 1];
       if (i < ohi - olo) {
-        const int64_t src = olo + i;
+        src = olo + i;
         if (src >= 0 && src < total_old)
-          val = old_rows[src * cpr + c];
+          kind = kOld;
         else
           raise_device_error(err, WNW_DEVERR_BOUNDS);
       } else {
-        val = new_rows[(int64_t)s * cpr + c];
+        src = s;
+        kind = kNew;
       }
     }
-    out[j * cpr + c] = val;
+    rs.kind[threadIdx.x] = kind;
+    rs.row[threadIdx.x] = src;
   }
+  __syncthreads();
+  copy_rows<false>(rs, nrows, cpr, old_rows, nullptr, nullptr, nullptr, new_rows, nullptr, B0, out, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -130,36 +187,40 @@ struct RebuildDesc {
   int32_t max_evict;
 };
 
-// Source of row i (relative) of a rebuilt segment.  kind: 0 old row, 1 load
-// row, 2 new token, 3 invalid descriptor (evict indices outside
-// [0, n_evict)).  Follows the reference's index arithmetic exactly:
-// kept_len subtracts the first min(n_evict, max_evict) ranges; an old row is
-// found by walking those ranges in order, skipping each range that starts
-// at or before the running source index.
+// Source of row i (relative) of a rebuilt segment: a RowKind (kNone for an
+// invalid descriptor: evict indices outside [0, n_evict)).  Follows the
+// reference's index arithmetic exactly: kept_len subtracts the first
+// min(n_evict, max_evict) ranges; an old row is found by walking those
+// ranges in order, skipping each range that starts at or before the running
+// source index.  The descriptor arrays reach the kernel inside a struct, so
+// they are read through global-address-space pointers.
 __device__ __forceinline__ int rebuild_source(const RebuildDesc& d, int s, int64_t old_len,
                                               int64_t i, int64_t& src) {
-  const int e0 = d.evict_offsets[s];
-  const int e1 = d.evict_offsets[s + 1];
+  const WNW_GLOBAL int32_t* eoff = gptr<int32_t>(d.evict_offsets);
+  const WNW_GLOBAL int32_t* est = gptr<int32_t>(d.evict_starts);
+  const WNW_GLOBAL int32_t* een = gptr<int32_t>(d.evict_ends);
+  const int e0 = eoff[s];
+  const int e1 = eoff[s + 1];
   const int ne = min(e1 - e0, d.max_evict);
-  if (ne > 0 && (e0 < 0 || (int64_t)e0 + ne > d.n_evict)) return 3;
+  if (ne > 0 && (e0 < 0 || (int64_t)e0 + ne > d.n_evict)) return kNone;
   int64_t kept = old_len;
-  for (int e = 0; e < ne; ++e) kept -= (int64_t)d.evict_ends[e0 + e] - d.evict_starts[e0 + e];
+  for (int e = 0; e < ne; ++e) kept -= (int64_t)een[e0 + e] - est[e0 + e];
   if (i < kept) {
     int64_t rel = i;
     for (int e = 0; e < ne; ++e) {
-      const int64_t es = d.evict_starts[e0 + e], ee = d.evict_ends[e0 + e];
+      const int64_t es = est[e0 + e], ee = een[e0 + e];
       if (rel >= es) rel += ee - es;
     }
     src = rel;
-    return 0;
+    return kOld;
   }
-  const int64_t ll = d.load_lens[s];
+  const int64_t ll = gptr<int32_t>(d.load_lens)[s];
   if (i < kept + ll) {
-    src = (int64_t)d.load_starts[s] + (i - kept);
-    return 1;
+    src = (int64_t)gptr<int32_t>(d.load_starts)[s] + (i - kept);
+    return kLoad;
   }
   src = s;
-  return 2;
+  return kNew;
 }
 
 __global__ __launch_bounds__(kNT) void rebuild_append_kernel(
@@ -170,47 +231,35 @@ __global__ __launch_bounds__(kNT) void rebuild_append_kernel(
     int64_t total_old, int64_t total_load, int64_t total_out, int cpr, u32x4* __restrict__ out_k,
     u32x4* __restrict__ out_v, int32_t* err) {
   __shared__ BlockSegs bs;
+  __shared__ RowSrc rs;
   const int64_t B0 = (int64_t)blockIdx.x * kRows;
   const int64_t B1 = min(B0 + kRows, total_out);
+  const int nrows = (int)(B1 - B0);
   scan_block_segments(new_cu, N, B0, B1, bs, err);
-  const int64_t nchunks = (B1 - B0) * cpr;
-  for (int64_t x = threadIdx.x; x < nchunks; x += kNT) {
-    const int64_t j = B0 + x / cpr;
-    const int c = (int)(x % cpr);
-    u32x4 vk = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
+  if ((int)threadIdx.x < nrows) {
+    const int64_t j = B0 + threadIdx.x;
+    int kind = kNone;
+    int64_t src = 0;
     if (bs.s_first > bs.s_last || j >= seg_hi(bs, new_cu, bs.s_last) || j < seg_lo(bs, new_cu, bs.s_first)) {
       raise_device_error(err, WNW_DEVERR_BOUNDS);
     } else {
       const int s = seg_of_row(bs, new_cu, j);
       const int64_t i = j - seg_lo(bs, new_cu, s);
       const int64_t olo = old_cu[s], ohi = old_cu[s + 1];
-      int64_t src = 0;
-      const int kind = rebuild_source(d, s, ohi - olo, i, src);
-      if (kind == 0) {
+      kind = rebuild_source(d, s, ohi - olo, i, src);
+      if (kind == kOld) {
         src += olo;
-        if (src >= 0 && src < total_old) {
-          vk = old_k[src * cpr + c];
-          vv = old_v[src * cpr + c];
-        } else {
-          raise_device_error(err, WNW_DEVERR_BOUNDS);
-        }
-      } else if (kind == 1) {
-        if (src >= 0 && src < total_load) {
-          vk = load_k[src * cpr + c];
-          vv = load_v[src * cpr + c];
-        } else {
-          raise_device_error(err, WNW_DEVERR_BOUNDS);
-        }
-      } else if (kind == 2) {
-        vk = new_k[src * cpr + c];
-        vv = new_v[src * cpr + c];
-      } else {
-        raise_device_error(err, WNW_DEVERR_BOUNDS);
+        if (src < 0 || src >= total_old) kind = kNone;
+      } else if (kind == kLoad) {
+        if (src < 0 || src >= total_load) kind = kNone;
       }
+      if (kind == kNone) raise_device_error(err, WNW_DEVERR_BOUNDS);
     }
-    out_k[j * cpr + c] = vk;
-    out_v[j * cpr + c] = vv;
+    rs.kind[threadIdx.x] = kind;
+    rs.row[threadIdx.x] = src;
   }
+  __syncthreads();
+  copy_rows<true>(rs, nrows, cpr, old_k, old_v, load_k, load_v, new_k, new_v, B0, out_k, out_v);
 }
 
 // ---------------------------------------------------------------------------
@@ -224,6 +273,7 @@ __global__ __launch_bounds__(kNT) void compact_segments_kernel(
     const int32_t* __restrict__ src_len, const int64_t* __restrict__ dst_base,
     const int32_t* __restrict__ new_len, RebuildDesc d, int with_new, int64_t src_rows,
     int64_t dst_rows, int64_t load_rows, int cpr, int32_t* err) {
+  __shared__ RowSrc rs;
   const int s = seg_list[blockIdx.y];
   if (s < 0 || s >= n_seg) {
     if (blockIdx.x == 0 && threadIdx.x == 0) raise_device_error(err, WNW_DEVERR_BOUNDS);
@@ -233,46 +283,32 @@ __global__ __launch_bounds__(kNT) void compact_segments_kernel(
   const int64_t r0 = (int64_t)blockIdx.x * kRows;
   if (r0 >= nl) return;
   const int64_t r1 = min(r0 + kRows, nl);
+  const int nrows = (int)(r1 - r0);
   const int64_t sb = src_base[s], sl = src_len[s], db = dst_base[s];
   if (db < 0 || db + nl > dst_rows || sb < 0 || sb + sl > src_rows) {
     if (threadIdx.x == 0) raise_device_error(err, WNW_DEVERR_BOUNDS);
     return;
   }
-  const int64_t nchunks = (r1 - r0) * cpr;
-  for (int64_t x = threadIdx.x; x < nchunks; x += kNT) {
-    const int64_t i = r0 + x / cpr;
-    const int c = (int)(x % cpr);
-    u32x4 vk = u32x4{0, 0, 0, 0}, vv = u32x4{0, 0, 0, 0};
+  if ((int)threadIdx.x < nrows) {
+    const int64_t i = r0 + threadIdx.x;
     int64_t src = 0;
     int kind = rebuild_source(d, s, sl, i, src);
-    if (kind == 2 && !with_new) kind = 3;  // row past kept + loaded: invalid
-    if (kind == 0) {
-      if (src >= 0 && src < sl) {
-        vk = src_k[(sb + src) * cpr + c];
-        vv = src_v[(sb + src) * cpr + c];
-      } else {
-        raise_device_error(err, WNW_DEVERR_BOUNDS);
-      }
-    } else if (kind == 1) {
-      if (src >= 0 && src < load_rows) {
-        vk = load_k[src * cpr + c];
-        vv = load_v[src * cpr + c];
-      } else {
-        raise_device_error(err, WNW_DEVERR_BOUNDS);
-      }
-    } else if (kind == 2) {
-      if (i == nl - 1) {
-        vk = new_k[(int64_t)s * cpr + c];
-        vv = new_v[(int64_t)s * cpr + c];
-      } else {
-        raise_device_error(err, WNW_DEVERR_BOUNDS);
-      }
-    } else {
-      raise_device_error(err, WNW_DEVERR_BOUNDS);
+    if (kind == kOld) {
+      if (src >= 0 && src < sl)
+        src += sb;
+      else
+        kind = kNone;
+    } else if (kind == kLoad) {
+      if (src < 0 || src >= load_rows) kind = kNone;
+    } else if (kind == kNew) {
+      if (!with_new || i != nl - 1) kind = kNone;  // only the last row is the new one
     }
-    dst_k[(db + i) * cpr + c] = vk;
-    dst_v[(db + i) * cpr + c] = vv;
+    if (kind == kNone) raise_device_error(err, WNW_DEVERR_BOUNDS);
+    rs.kind[threadIdx.x] = kind;
+    rs.row[threadIdx.x] = src;
   }
+  __syncthreads();
+  copy_rows<true>(rs, nrows, cpr, src_k, src_v, load_k, load_v, new_k, new_v, db + r0, dst_k, dst_v);
 }
 
 // ---------------------------------------------------------------------------
@@ -330,9 +366,9 @@ extern "C" int wnw_interleave_append(const void* old_rows, const void* new_rows,
   WNW_CHECK_ARG(aligned16(old_rows) && aligned16(new_rows) && aligned16(out), "rows must be 16-byte aligned");
   const int64_t blocks = (total_out + kRows - 1) / kRows;
   WNW_CHECK_ARG(blocks < (1ll << 31), "too many rows");
-  hipLaunchKernelGGL(interleave_append_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream,
-                     (const u32x4*)old_rows, (const u32x4*)new_rows, cu_old, cu_new, (int)n_seg, total_old,
-                     total_out, cpr, (u32x4*)out, device_error_word());
+  hipLaunchKernelGGL(interleave_append_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream, (const u32x4*)old_rows,
+                     (const u32x4*)new_rows, cu_old, cu_new, (int)n_seg, total_old, total_out, cpr, (u32x4*)out,
+                     device_error_word());
   WNW_CHECK_HIP(hipGetLastError(), "interleave_append launch");
   return WNW_OK;
 }
@@ -389,10 +425,10 @@ extern "C" int wnw_rebuild_append_kv(const void* old_k, const void* old_v, const
   d.evict_ends = evict_ends;
   d.n_evict = n_evict;
   d.max_evict = (int32_t)std::max<int64_t>(std::min<int64_t>(max_evict, 1 << 30), 1);
-  hipLaunchKernelGGL(rebuild_append_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream,
-                     (const u32x4*)old_k, (const u32x4*)old_v, (const u32x4*)new_k, (const u32x4*)new_v,
-                     (const u32x4*)load_k, (const u32x4*)load_v, old_cu, new_cu, d, (int)n_seg, total_old,
-                     total_load, total_out, cpr, (u32x4*)out_k, (u32x4*)out_v, device_error_word());
+  hipLaunchKernelGGL(rebuild_append_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream, (const u32x4*)old_k,
+                     (const u32x4*)old_v, (const u32x4*)new_k, (const u32x4*)new_v, (const u32x4*)load_k,
+                     (const u32x4*)load_v, old_cu, new_cu, d, (int)n_seg, total_old, total_load, total_out, cpr,
+                     (u32x4*)out_k, (u32x4*)out_v, device_error_word());
   WNW_CHECK_HIP(hipGetLastError(), "rebuild_append_kv launch");
   return WNW_OK;
 }

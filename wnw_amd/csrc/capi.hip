@@ -45,6 +45,19 @@ int32_t* device_error_word() {
   return g_err_words[dev];
 }
 
+int device_cus() {
+  static std::vector<int> cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lock(g_mu);
+  if ((int)cus.size() <= dev) cus.resize(dev + 1, 0);
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 }  // namespace wnw
 
 extern "C" const char* wnw_last_error(void) { return wnw::g_err; }

@@ -338,15 +338,7 @@ static const void* score_fn_d(int which, int64_t D, int iters) {
 // max_audio rows: 16 iterations when that still gives two workgroups per CU,
 // else 4 (more, shorter workgroups).
 static int score_iters(int64_t max_audio, int64_t ny, int64_t head_dim, int elem_bytes) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
-                                                 hipSuccess && n > 0)
-      cus = n;
-    else
-      cus = 256;
-  }
+  const int cus = device_cus();
   const int64_t rows16 = score_rows_per_wg((int)head_dim, elem_bytes, kIters);
   return ((max_audio + rows16 - 1) / rows16) * ny >= 2 * (int64_t)cus ? kIters : kItersSmall;
 }

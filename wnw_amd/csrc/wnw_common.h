@@ -16,6 +16,9 @@ void set_error(const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 // Per-device error word (allocated once per device by the library).
 int32_t* device_error_word();
+// Compute units of the current device (queried once per device; 256 when
+// the query fails).
+int device_cus();
 
 #define WNW_CHECK_ARG(cond, ...)       \
   do {                                 \
