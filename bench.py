@@ -21,6 +21,10 @@ Reported:
 * roofline       -- the attention kernel: algorithmic bytes per launch /
                     average launch time vs 8 TB/s.
 * append_us_per_layer_step -- the in-place append kernel alone, per layer-step.
+* compaction     -- the rebuild (compaction + append) kernel on the dense
+                    layout, per layer: class-B segments drop their oldest
+                    window row, every segment gets a new row; µs per layer
+                    and TB/s of rows moved.
 * cpu_baseline   -- the float64 C oracle (1 core) on a bounded sample of the
                     same layers.
 
@@ -275,6 +279,10 @@ def main():
     append_us = ev2.elapsed_time(ev3) * 1e3 / (2 * app_reps * L)
     assert _lib.device_error() == 0, "device error during append timing"
 
+    # ---- compaction timing: one rebuild (a4) per layer ---------------------
+    compact = compaction_timing(cfg, layers, dev, stream, graphs is not None)
+    assert _lib.device_error() == 0, "device error during compaction timing"
+
     # ---- CPU baseline: float64 C oracle on a bounded sample ---------------
     cpu = None
     if not args.no_cpu:
@@ -298,12 +306,74 @@ def main():
                    "kernel": args.kernel, "graph": graphs is not None, "notes": cfg.notes},
         "us_per_layer_step": round(us_per_launch, 3),
         "append_us_per_layer_step": round(append_us, 3),
+        "compaction": compact,
         "attn_TBs": round(achieved_gbs / 1e3, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def compaction_timing(cfg, layers, dev, stream, use_graph: bool, reps: int = 5) -> dict:
+    """One ``rebuild_append_kv`` per layer on the dense layout (the reference's
+    layout): every class-B segment drops row 4 (sink + window: the oldest
+    window row, one relative evict range [4, 5)), every segment gets the
+    step's new row, nothing is loaded.  Bytes = rows moved: the kept and new
+    rows read, every output row written, K and V."""
+    import numpy as np
+    import torch
+
+    from wnw_amd.wnw.kernels import rebuild_append_kv
+
+    D = cfg.head_dim
+    i32 = dict(dtype=torch.int32, device=dev)
+    calls, moved = [], 0
+    for li, st in enumerate(layers):
+        lens = st.lens0.astype(np.int64)
+        base = st.base.cpu().numpy()
+        idx = torch.from_numpy(np.concatenate([b + np.arange(n) for b, n in zip(base, lens)])).to(dev)
+        dk, dv = st.k.index_select(0, idx), st.v.index_select(0, idx)
+        class_b = ~np.tile(cfg.class_a[li].astype(bool), cfg.batch)
+        n_ev = class_b.astype(np.int64)
+        old_cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        new_lens = lens - n_ev + 1
+        new_cu = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+        ev_off = np.concatenate([[0], np.cumsum(n_ev)]).astype(np.int32)
+        n_b = int(n_ev.sum())
+        args = (dk, dv, st.new_k, st.new_v, dk[:0], dv[:0], torch.from_numpy(old_cu).to(dev),
+                torch.from_numpy(new_cu).to(dev), torch.full((st.n,), -1, **i32), torch.zeros(st.n, **i32),
+                torch.from_numpy(ev_off).to(dev), torch.full((n_b,), 4, **i32), torch.full((n_b,), 5, **i32), 1)
+        calls.append((args, int(new_cu[-1])))
+        moved += int(new_cu[-1]) * D * 2 * 2 * 2
+    torch.cuda.synchronize()
+
+    def launches():
+        for args, tot in calls:
+            rebuild_append_kv(*args, total_out=tot)
+
+    with torch.cuda.stream(stream):
+        launches()  # allocates the outputs before capture
+        graph = None
+        if use_graph:
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                launches()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        (graph.replay if graph is not None else launches)()
+        e0.record(stream)
+        for _ in range(reps):
+            (graph.replay if graph is not None else launches)()
+        e1.record(stream)
+        e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+    bytes_per_launch = moved / len(layers)
+    return {"kernel": "rebuild_append_kernel", "us_per_layer_step": round(us, 3),
+            "bytes_per_launch": int(bytes_per_launch),
+            "TBs": round(bytes_per_launch / (us * 1e-6) / 1e12, 3),
+            "frac_of_peak": round(bytes_per_launch / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "workload": "dense layout, class-B segments drop row 4 (evict [4, 5)), one new row per segment"}
 
 
 def traffic_from_profiles(workload: str):
