@@ -70,6 +70,7 @@ struct SchedLds {
   int32_t P;       // effective number of workgroups (<= R)
   int32_t s_first, s_last;
   int32_t is_last;  // combine flag broadcast
+  alignas(16) int32_t hdr[16][4];  // streaming kernel: merge slot headers (segment, length, base lo, base hi)
   int64_t ring_base[kRing];
   int32_t ring_len[kRing];
 };
@@ -328,6 +329,16 @@ __device__ __forceinline__ bool arrive(const AttnParams& p, const SchedLds& sl, 
   return old == (int)(p_last - p_first);
 }
 
+// The merge of segment s from its np pieces, the first held by workgroup
+// p_first (by threads t = 0 .. nt - 1), and the reset of its counter for the
+// next launch.
+template <typename T>
+__device__ __forceinline__ void combine_from(const AttnParams& p, int D, int64_t p_first, int np, int s, int t,
+                                             int nt) {
+  combine_pieces<T>(p, D, p_first + s /* slot of the first piece */, np, s, t, nt);
+  if (t == 0) __hip_atomic_store(gptr_w<int32_t>(p.counters) + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The last arriver of segment s merges every partial into the output (by
 // threads t = 0 .. nt - 1 of the workgroup) and resets the counter for the
 // next launch.  No LDS is used.
@@ -336,9 +347,7 @@ __device__ __forceinline__ void combine_segment(const AttnParams& p, int D, cons
                                                 int64_t seg_len, int s, int t, int nt) {
   int64_t p_first, p_last;
   piece_range(sl, seg_base, seg_len, p_first, p_last);
-  const int np = (int)(p_last - p_first + 1);
-  combine_pieces<T>(p, D, p_first + s /* slot of the first piece */, np, s, t, nt);
-  if (t == 0) __hip_atomic_store(gptr_w<int32_t>(p.counters) + s, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  combine_from<T>(p, D, p_first, (int)(p_last - p_first + 1), s, t, nt);
 }
 
 // Arrival of this workgroup's partial of segment s followed, on the last
@@ -779,7 +788,12 @@ struct StreamGeom {
   static constexpr int CH = RB / 16;           // 16-byte chunks per row
   static constexpr int NC = D / 32;            // QK k-chunks
   static constexpr int NTD = D / 16;           // PV output tiles
-  static constexpr int kSlot = 16 + 2 * kMaxGroupS * 4 + kMaxGroupS * D * 4;  // merge slot bytes
+  // Merge slot: (m, l) per head, then one accumulator row per head (the
+  // slot's header lives in SchedLds::hdr).
+  // Rows are DP floats apart, DP = 20 (mod 64): the (up to 8) heads a wave
+  // writes in one instruction then start in different groups of 4 LDS banks.
+  static constexpr int DP = D + 20;
+  static constexpr int kSlot = 2 * kMaxGroupS * 4 + kMaxGroupS * DP * 4;  // merge slot bytes
 };
 
 // LDS bytes of the streaming kernel: per wave two (K, V) step buffers and two
@@ -1079,21 +1093,23 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   // ---- shared pieces: merge the waves' states through LDS
   __syncthreads();  // every wave is done with its step buffers (reused below)
   constexpr int SLOT = G_::kSlot;
+  static_assert(2 * NW * SLOT <= NW * 4 * SB, "the merge slots reuse the step buffers");
   auto slot_of = [&](int i) { return dyn + i * SLOT; };
   auto put = [&](int i, int32_t s, int64_t b, int32_t len, float m, float l, const f32x4* a) {
     uint8_t* sp = slot_of(i);
     if (lane == 0) {
-      *(int32_t*)sp = s;
-      *(int32_t*)(sp + 4) = len;
-      *(int64_t*)(sp + 8) = b;
+      sl.hdr[i][0] = s;
+      sl.hdr[i][1] = len;
+      sl.hdr[i][2] = (int32_t)(uint32_t)b;
+      sl.hdr[i][3] = (int32_t)(b >> 32);
     }
     if (s >= 0 && lc < G) {
-      float* ml = (float*)(sp + 16);
+      float* ml = (float*)sp;
       if (lq == 0) {
         ml[lc] = m;
         ml[kMaxGroupS + lc] = l;
       }
-      float* ap = (float*)(sp + 16 + 2 * kMaxGroupS * 4) + lc * D;
+      float* ap = (float*)(sp + 2 * kMaxGroupS * 4) + lc * G_::DP;
 #pragma unroll
       for (int t = 0; t < NTD; ++t) *(f32x4*)(ap + 16 * t + 4 * lq) = a[t];
     }
@@ -1101,18 +1117,23 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   put(2 * w, h_s, h_b, h_len, m_h, l_h, acc_h);
   put(2 * w + 1, c_s, c_b, c_len, m_run, l_run, acc);
   __syncthreads();
-  // Slot headers, read once by every thread (one address for all lanes, so
-  // the values are uniform).  Slots follow the row order, and segments are
-  // disjoint and ordered, so the slots of one segment are consecutive (empty
-  // slots aside); a slot leads when no earlier slot holds its segment.
+  // Slot headers: lane i reads header i % NS (one LDS read for all of
+  // them), then every header is broadcast from its lane into scalars.
+  // Slots follow the row order, and segments are disjoint and ordered, so
+  // the slots of one segment are consecutive (empty slots aside); a slot
+  // leads when no earlier slot holds its segment.
   constexpr int NS = 2 * NW;
+  static_assert(NS <= 16, "merge slot headers");
+  typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+  const i32x4 hv = *(const i32x4*)sl.hdr[lane % NS];
   int32_t ss[NS], sn[NS];
   int64_t sb[NS];
 #pragma unroll
   for (int i = 0; i < NS; ++i) {
-    ss[i] = uni(*(const int32_t*)slot_of(i));
-    sn[i] = uni(*(const int32_t*)(slot_of(i) + 4));
-    sb[i] = uni(*(const int64_t*)(slot_of(i) + 8));
+    ss[i] = __builtin_amdgcn_readlane(hv.x, i);
+    sn[i] = __builtin_amdgcn_readlane(hv.y, i);
+    sb[i] = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hv.w, i) << 32) |
+                      (uint32_t)__builtin_amdgcn_readlane(hv.z, i));
   }
   // Per leader: the slots of its segment (bit mask).  At most two segments
   // cross the workgroup's range boundaries (segments are disjoint); those
@@ -1155,10 +1176,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
       f32x4 av[NS];
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
-        const float* ml = (const float*)(slot_of(j) + 16);
+        const float* ml = (const float*)slot_of(j);
         mv[j] = ml[g];
         lv[j] = ml[kMaxGroupS + g];
-        av[j] = *(const f32x4*)((const float*)(slot_of(j) + 16 + 2 * kMaxGroupS * 4) + 4 * i4);
+        av[j] = *(const f32x4*)((const float*)(slot_of(j) + 2 * kMaxGroupS * 4) + g * G_::DP + (4 * i4 - g * D));
       }
       float M = kNegBig;
 #pragma unroll
@@ -1201,13 +1222,32 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
       }
     }
   }
+  // piece counts of the partial segments, worked out while the stores drain
+  int32_t pn0 = 0, pn1 = 0;  // pieces - 1
+  int64_t pf0 = 0, pf1 = 0;  // workgroup of the first piece
+  {
+    int64_t l;
+    if (ps0 >= 0) {
+      piece_range(sl, pb0, pl0, pf0, l);
+      pn0 = (int32_t)(l - pf0);
+    }
+    if (ps1 >= 0) {
+      piece_range(sl, pb1, pl1, pf1, l);
+      pn1 = (int32_t)(l - pf1);
+    }
+  }
   wait_vmem();
   __syncthreads();  // partials complete; the slots may be overwritten below
-  // both arrivals at once; each segment whose last partial this is merges
-  if (tid == 0) {
-    const int f0 = ps0 >= 0 && arrive(p, sl, pb0, pl0, ps0);
-    const int f1 = ps1 >= 0 && arrive(p, sl, pb1, pl1, ps1);
-    sl.is_last = f0 | (f1 << 1);
+  // Both arrivals in one atomic instruction (lanes 0 and 1 of wave 0, one
+  // memory round trip); each segment whose last partial this is merges.
+  if (tid < 2) {
+    const int32_t ps = tid ? ps1 : ps0;
+    bool f = false;
+    if (ps >= 0)
+      f = __hip_atomic_fetch_add(gptr_w<int32_t>(p.counters) + ps, 1, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == (tid ? pn1 : pn0);
+    const uint64_t fl = __ballot(f);
+    if (tid == 0) sl.is_last = (int)(fl & 3);
   }
   __syncthreads();
   // the segments this workgroup completes are merged side by side (one
@@ -1217,7 +1257,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     const bool both = last == 3;
     const int nt = both ? NT / 2 : NT;
     const bool k = both ? tid >= NT / 2 : last == 2;  // uniform per wave
-    combine_segment<T>(p, D, sl, k ? pb1 : pb0, k ? pl1 : pl0, k ? ps1 : ps0, both && k ? tid - NT / 2 : tid, nt);
+    combine_from<T>(p, D, k ? pf1 : pf0, (k ? pn1 : pn0) + 1, k ? ps1 : ps0, both && k ? tid - NT / 2 : tid, nt);
   }
 }
 
