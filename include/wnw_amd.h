@@ -231,11 +231,14 @@ int wnw_decode_attn_ex(const void* q, const void* k, const void* v,
 /* Class-A token scores                                                      */
 /* ------------------------------------------------------------------------ */
 
-/* Workspace of wnw_decode_attn_score: the attention workspace followed by
- * the per-segment softmax normalisers.  Same clearing rule as the attention
- * workspace (wnw_workspace_init once, again whenever n_seg changes). */
+/* Workspace of wnw_decode_attn_score: the attention workspace, the
+ * per-segment softmax normalisers, then (max_audio > 0) room for the logits
+ * of the scored audio rows, n_seg * group * max_audio floats.  Same clearing
+ * rule as the attention workspace (wnw_workspace_init once, again whenever
+ * n_seg changes).  A workspace sized with max_audio = 0 still works: the
+ * scoring pass then reads the K rows again. */
 int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group,
-                                              int64_t head_dim);
+                                              int64_t head_dim, int64_t max_audio);
 
 /*
  * Decode attention + class-A score accumulation, the reference's
@@ -251,6 +254,11 @@ int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group,
  * sum is deterministic).  max_audio >= every audio_ends[b] - audio_starts[b]
  * (it sizes the grid); acc_len = entries of score_acc.  Audio ranges outside
  * a segment set WNW_DEVERR_BOUNDS and skip that segment.
+ * When the streaming attention kernel runs (bf16/f16, head_dim 64/128,
+ * group <= 8) and the workspace has room for the logits (see
+ * wnw_decode_attn_score_workspace_bytes), the attention kernel keeps the
+ * scaled logits of the scored rows and the scoring pass reads those instead
+ * of K (4 bytes per row and head instead of 2 * head_dim).
  */
 int wnw_decode_attn_score(const void* q, const void* k, const void* v,
                           const int32_t* cu_k, const int64_t* seg_base,

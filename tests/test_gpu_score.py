@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 S_ATOL, S_RTOL = 1e-6, 1e-3
 
 
-def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_rows=None, kv_scale=1.0):
+def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_rows=None, kv_scale=1.0,
+                     keep_logits=True):
     rng = np.random.default_rng(seed)
     n = len(lens)
     B = n // H
@@ -37,28 +38,33 @@ def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_r
                                  base=base, dtype=oracle.DT_BF16)
     t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
     acc = torch.from_numpy(acc0).to(dev)
-    print(f"attn_score n_seg={n} H={H} G={G} D={D} mask={mask} seed={seed}", flush=True)
+    print(f"attn_score n_seg={n} H={H} G={G} D={D} mask={mask} seed={seed} keep_logits={keep_logits}", flush=True)
     out = fused_attn.q1_decode_attn_score(
         to_torch(q, "bfloat16", dev), to_torch(k, "bfloat16", dev), to_torch(v, "bfloat16", dev), t(cu), scale,
         t(mask), H, t(a_s), t(a_e), acc, t(offs),
-        seg_base=None if base is None else t(base, torch.int64), max_audio=int(max(np.array(a_e) - np.array(a_s))))
+        seg_base=None if base is None else t(base, torch.int64), max_audio=int(max(np.array(a_e) - np.array(a_s))),
+        keep_logits=keep_logits)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
     got_out = oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16)
     return got_out, ref_out, acc.cpu().numpy().astype(np.float64), ref_acc
 
 
-def test_attn_score_small():
+# keep_logits: the attention kernel keeps the scored rows' logits (streaming
+# kernel) or the scoring pass reads K again; both must match the oracle.
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_small(keep_logits):
     lens = [40, 300, 17, 1000, 64, 2, 513, 90]  # B = 2, H = 4
     got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 4, 4, 128, [0, 1, 0, 1],
-                                            [3, 0], [17, 2], seed=1)
+                                            [3, 0], [17, 2], seed=1, keep_logits=keep_logits)
     ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
     assert ok, msg
     ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
     assert ok, msg
 
 
-def test_attn_score_slack_layout_and_group7():
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_slack_layout_and_group7(keep_logits):
     lens = [500, 33, 260, 70]  # B = 2, H = 2
     caps = [520, 40, 300, 80]
     base = np.zeros(4, np.int64)
@@ -67,14 +73,16 @@ def test_attn_score_slack_layout_and_group7():
         base[s] = pos
         pos += caps[s] + 3
     got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 2, 7, 128, [1, 0], [10, 5],
-                                            [480, 250], seed=2, base=base, pool_rows=pos + 4)
+                                            [480, 250], seed=2, base=base, pool_rows=pos + 4,
+                                            keep_logits=keep_logits)
     ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
     assert ok, msg
     ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
     assert ok, msg
 
 
-def test_attn_score_cfg2_layer():
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_cfg2_layer(keep_logits):
     """One cfg2 layer at full size: class-A segments hold 7,500 audio rows."""
     cfg = workloads.config2()
     lens = cfg.lengths[0] + 1
@@ -82,7 +90,8 @@ def test_attn_score_cfg2_layer():
     mask = cfg.class_a[0].astype(np.int32).tolist()
     a_s, a_e = [0] * cfg.batch, [7500] * cfg.batch
     got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, cfg.group, cfg.head_dim, mask,
-                                            a_s, a_e, seed=3, kv_scale=float(cfg.kv_scale[0].mean()))
+                                            a_s, a_e, seed=3, kv_scale=float(cfg.kv_scale[0].mean()),
+                                            keep_logits=keep_logits)
     ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
     assert ok, msg
     ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
@@ -132,13 +141,38 @@ def test_score_bad_audio_range_is_flagged():
     assert _lib.device_error() == 0
 
 
-def test_attn_score_many_samples():
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_bad_audio_range_is_flagged(keep_logits):
+    """A flagged segment whose audio range ends past the segment sets the
+    device error word; that sample's tokens are left untouched, the other
+    sample is scored."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(14)
+    lens = [100, 50, 80, 60]  # B = 2, H = 2; KV head 0 is flagged
+    cu = cu_from_lens(lens)
+    q = to_torch(rand_rows(rng, 4 * 4, 64, "bfloat16").reshape(4, 4, 64), "bfloat16", dev)
+    k = to_torch(rand_rows(rng, int(cu[-1]), 64, "bfloat16"), "bfloat16", dev)
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)  # noqa: E731
+    acc = torch.zeros(170, device=dev)
+    print(f"attn_score bad audio range keep_logits={keep_logits}", flush=True)
+    fused_attn.q1_decode_attn_score(q, k, k, t(cu), 0.125, t([1, 0]), 2, t([0, 10]), t([120, 60]), acc,
+                                    t([0, 120, 170]), max_audio=120, keep_logits=keep_logits)
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_BOUNDS
+    assert float(acc[:120].abs().sum()) == 0.0  # sample 0: 120 audio rows in a 100-row segment
+    assert float(acc[120:170].min()) > 0.0      # sample 1: scored
+    assert _lib.device_error() == 0
+
+
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_many_samples(keep_logits):
     """Enough samples x audio rows for the long (16-iteration) scoring workgroups."""
     rng = np.random.default_rng(12)
     B, H = 24, 2
     lens = [int(x) for x in rng.integers(6000, 6100, size=B * H)]
     a_s, a_e = [0] * B, [6000] * B
-    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, 4, 128, [1, 0], a_s, a_e, seed=12)
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, 4, 128, [1, 0], a_s, a_e, seed=12,
+                                            keep_logits=keep_logits)
     ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
     assert ok, msg
     ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)

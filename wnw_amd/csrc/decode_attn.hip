@@ -61,6 +61,16 @@ struct AttnParams {
   int32_t n_seg;
   int32_t G;
   float scale_log2;  // scale * log2(e)
+  // Streaming kernel only, null otherwise: the scaled logits (log2 domain)
+  // of the audio rows of the segments whose KV head is flagged, for the
+  // class-A scoring pass: xlog[(s * G + g) * max_audio + t] for audio row t
+  // (relative to audio_s[s / Hkv]) of segment s, t < max_audio.
+  float* xlog;
+  const int32_t* xmask;    // [Hkv] non-zero: KV head scored
+  const int32_t* audio_s;  // [n_seg / Hkv] audio range of each sample, relative to its segments' starts
+  const int32_t* audio_e;
+  int64_t max_audio;
+  int32_t Hkv;
 };
 
 // Per-workgroup schedule, shared through LDS.
@@ -73,6 +83,8 @@ struct SchedLds {
   alignas(16) int32_t hdr[16][4];  // streaming kernel: merge slot headers (segment, length, base lo, base hi)
   int64_t ring_base[kRing];
   int32_t ring_len[kRing];
+  int32_t ring_a0[kRing];    // with xlog: audio start of the segment
+  int32_t ring_alen[kRing];  // with xlog: audio rows kept (0: segment not scored)
 };
 
 __device__ __forceinline__ int64_t range_start(int64_t p, int64_t R, int64_t P) {
@@ -90,7 +102,7 @@ __device__ __forceinline__ int64_t effective_wgs(int64_t R) {
 // loads) finds the segments whose rows overlap this workgroup's range,
 // checks the layout, and writes the outputs of empty segments (zeros) and of
 // invalid ones (NaN) owned by this workgroup (segment i -> workgroup i % grid).
-template <typename T, int NT>
+template <typename T, int NT, bool XL = false>
 __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
   const int tid = threadIdx.x;
   const int N = p.n_seg;
@@ -106,6 +118,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   const int64_t B1 = active ? range_start(pid + 1, R, P) : 0;
   int32_t lo[4], hi[4], nxt[4];
   int64_t bs[4], bn[4];
+  int32_t xm[4], xa[4], xe[4];  // with xlog: KV-head flag, audio range
   const WNW_GLOBAL int32_t* cu = gptr<int32_t>(p.cu);
   const WNW_GLOBAL int64_t* basep = gptr<int64_t>(p.base);
   auto load_chunk = [&](int i0) {
@@ -114,6 +127,12 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       const int i = i0 + u * NT + tid;
       lo[u] = hi[u] = nxt[u] = 0;
       bs[u] = bn[u] = 0;
+      xm[u] = xa[u] = xe[u] = 0;
+      if (XL && i < N) {
+        xm[u] = gptr<int32_t>(p.xmask)[i % p.Hkv];
+        xa[u] = gptr<int32_t>(p.audio_s)[i / p.Hkv];
+        xe[u] = gptr<int32_t>(p.audio_e)[i / p.Hkv];
+      }
       if (i < N) {
         lo[u] = cu[i];
         hi[u] = cu[i + 1];
@@ -132,6 +151,10 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   if (tid < kRing) {
     sl.ring_base[tid] = 0;
     sl.ring_len[tid] = 0;
+    if (XL) {
+      sl.ring_a0[tid] = 0;
+      sl.ring_alen[tid] = 0;
+    }
   }
   // The loads of the first chunk are issued before the barrier: one global
   // round trip for n_seg <= 4 * NT.
@@ -173,6 +196,10 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
         atomicMax(&sl.s_last, i);
         sl.ring_base[i % kRing] = b;
         sl.ring_len[i % kRing] = (int32_t)len;
+        if (XL) {
+          sl.ring_a0[i % kRing] = xa[u];
+          sl.ring_alen[i % kRing] = xm[u] ? (int32_t)max((int64_t)0, min((int64_t)xe[u] - xa[u], p.max_audio)) : 0;
+        }
       }
     }
   }
@@ -808,9 +835,11 @@ struct SStep {
   int64_t seg_b;
   int32_t s, nrows, seg_len, qslot;
   int32_t first, last, whole;
+  int32_t t0, alen;  // audio index of the first row; audio rows whose logits are kept (0: none)
 };
 
-template <typename T, int D, int NW, int QD>
+// XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
+template <typename T, int D, int NW, int QD, bool XL>
 __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   using G_ = StreamGeom<D>;
   using Ops = StreamOps<T>;
@@ -853,7 +882,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
       dma_copy16(src, (uint32_t)(rr * RB + (((lane % CH) ^ sw) * 16)), dst + u * 1024);
     }
   };
-  schedule<T, NT>(p, D, sl);
+  schedule<T, NT, XL>(p, D, sl);
   if (sl.s_first > sl.s_last) return;
   const int64_t R = uni(sl.R);
   const int64_t B0 = uni(sl.B0), B1 = uni(sl.B1);
@@ -865,20 +894,29 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   // the valid ones overlapping [W0, W1) that are not taken yet.
   int wb = s_first;
   int64_t lb = 0;
-  int32_t llen = 0;
+  int32_t llen = 0, la0 = 0, lal = 0;
   uint64_t mask = 0;
   auto load_window = [&]() {
     const int s = wb + lane;
     lb = 0;
     llen = 0;
+    la0 = lal = 0;
     if (s <= s_last) {
       if (in_ring) {
         lb = sl.ring_base[s % kRing];
         llen = sl.ring_len[s % kRing];
+        if (XL) {
+          la0 = sl.ring_a0[s % kRing];
+          lal = sl.ring_alen[s % kRing];
+        }
       } else {
         const int32_t lo = p.cu[s], hi = p.cu[s + 1];
         lb = p.base ? p.base[s] : (int64_t)lo;
         llen = hi - lo;
+        if (XL && p.xmask[s % p.Hkv]) {
+          la0 = p.audio_s[s / p.Hkv];
+          lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
+        }
       }
     }
     // the piece [max(lb, W0), min(lb + len, W1)) must be non-empty (an empty
@@ -888,7 +926,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   };
   load_window();
   // issue-side iterator: current piece [pb, pe) of segment cur_s
-  int cur_s = 0, cur_len = 0, piece_no = 0;
+  int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0;
   int64_t cur_b = 0, pb = 0, pe = 0, irow = 0;
   bool cur_whole = false, have = false;
   auto next_piece = [&]() {
@@ -907,6 +945,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)lb >> 32), k);
     cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
     cur_len = __builtin_amdgcn_readlane(llen, k);
+    if (XL) {
+      cur_a0 = __builtin_amdgcn_readlane(la0, k);
+      cur_al = __builtin_amdgcn_readlane(lal, k);
+    }
     pb = max(cur_b, W0);
     pe = min(cur_b + cur_len, W1);
     cur_whole = cur_b >= W0 && cur_b + cur_len <= W1;
@@ -924,6 +966,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     st.first = irow == pb;
     st.whole = cur_whole;
     st.qslot = piece_no & 1;
+    if (XL) {
+      st.t0 = (int32_t)(irow - cur_b) - cur_a0;
+      st.alen = cur_al;
+    }
     irow += kSRows;
     st.last = irow >= pe;
     if (st.last) {
@@ -989,6 +1035,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     for (int i = 0; i < 4; ++i) {
       x[i] = (4 * lq + i) < st.nrows ? sacc[i] * p.scale_log2 : -INFINITY;
       mx = fmaxf(mx, x[i]);
+    }
+    if (XL && st.alen > 0 && st.t0 < st.alen && st.t0 + st.nrows > 0 && lc < G) {
+      // rows of a scored segment's audio: keep their logits for the scoring pass
+      WNW_GLOBAL float* xl = gptr_w<float>(p.xlog) + ((int64_t)st.s * G + lc) * p.max_audio;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * lq + i, t = st.t0 + r;
+        if (r < st.nrows && t >= 0 && t < st.alen) xl[t] = x[i];
+      }
     }
     mx = fmaxf(mx, swap16(mx));
     mx = fmaxf(mx, swap32(mx));
@@ -1439,18 +1494,18 @@ __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
 
 // Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
 // stream_lds_bytes (above 64 KB, so the limit is raised once per instance).
-template <typename T, int D, int QD>
+template <typename T, int D, int QD, bool XL>
 static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
   const int qslot = (ap.G * D * 2 + 255) & ~255;
   const int lds = stream_lds_bytes(D, kNW, qslot);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)&attn_stream_kernel<T, D, kNW, QD>,
+    attr_err = hipFuncSetAttribute((const void*)&attn_stream_kernel<T, D, kNW, QD, XL>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes(D, kNW, 2048));
   });
   if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap);
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap);
   return hipGetLastError();
 }
 
@@ -1459,7 +1514,11 @@ static hipError_t launch_attn(int kernel, const AttnParams& ap, int64_t n_wg, hi
   if (kernel == WNW_ATTN_STREAM) {
     if constexpr (sizeof(T) == 2 && (D == 64 || D == 128)) {
       const int qd = (ap.G * D * 2 + 1023) / 1024;
-      if (ap.G <= kMaxGroupS) return qd == 1 ? launch_stream<T, D, 1>(ap, n_wg, st) : launch_stream<T, D, 2>(ap, n_wg, st);
+      if (ap.G <= kMaxGroupS) {
+        if (ap.xlog)
+          return qd == 1 ? launch_stream<T, D, 1, true>(ap, n_wg, st) : launch_stream<T, D, 2, true>(ap, n_wg, st);
+        return qd == 1 ? launch_stream<T, D, 1, false>(ap, n_wg, st) : launch_stream<T, D, 2, false>(ap, n_wg, st);
+      }
     }
     return hipErrorInvalidValue;
   }
@@ -1506,13 +1565,12 @@ extern "C" int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void
 }
 
 namespace wnw {
-// Shared by the public attention entry points; lse (optional) receives each
-// segment's final softmax (max, sum) in the log2 domain, [n_seg, G, 2].
 int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
                      const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     void* stream) {
+                     const AttnLogits* logits, int* logits_kept, void* stream) {
+  if (logits_kept) *logits_kept = 0;
   WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1ll << 30), "n_seg out of range: %lld", (long long)n_seg);
   if (n_seg == 0) return WNW_OK;
   WNW_CHECK_ARG(q && cu_k && out && workspace && ((k && v) || kv_rows == 0), "null pointer argument");
@@ -1569,6 +1627,22 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   ap.n_seg = (int32_t)n_seg;
   ap.G = (int32_t)group;
   ap.scale_log2 = scale * kLog2e;
+  ap.xlog = nullptr;
+  ap.xmask = ap.audio_s = ap.audio_e = nullptr;
+  ap.max_audio = 0;
+  ap.Hkv = 1;
+  if (logits && kern == WNW_ATTN_STREAM) {
+    WNW_CHECK_ARG(logits->xlog && logits->mask && logits->audio_s && logits->audio_e, "null logits argument");
+    WNW_CHECK_ARG(logits->hkv >= 1 && n_seg % logits->hkv == 0 && logits->max_audio > 0,
+                  "bad logits geometry");
+    ap.xlog = logits->xlog;
+    ap.xmask = logits->mask;
+    ap.audio_s = logits->audio_s;
+    ap.audio_e = logits->audio_e;
+    ap.max_audio = logits->max_audio;
+    ap.Hkv = logits->hkv;
+    if (logits_kept) *logits_kept = 1;
+  }
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = hipErrorInvalidValue;
   switch (dtype) {
@@ -1588,7 +1662,8 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
                                   int dtype, void* out, void* workspace, int64_t workspace_bytes,
                                   int kernel, int64_t n_wg, void* stream) {
   return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
-                          dtype, out, workspace, workspace_bytes, kernel, n_wg, nullptr, stream);
+                          dtype, out, workspace, workspace_bytes, kernel, n_wg, nullptr, nullptr, nullptr,
+                          stream);
 }
 
 extern "C" int wnw_decode_attn(const void* q, const void* k, const void* v, const int32_t* cu_k,

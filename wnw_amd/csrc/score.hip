@@ -28,12 +28,6 @@
 
 namespace wnw {
 
-int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
-                     const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
-                     int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
-                     void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     void* stream);
-
 static constexpr int kScoreThreads = 256;
 // Row iterations per scoring workgroup: 16, or 4 when 16 would leave CUs idle
 // (few samples or short audio).
@@ -162,6 +156,63 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
       if (j < n_audio) p.acc[off + j] += total[it];
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// scores from the logits the streaming attention kernel kept
+// ---------------------------------------------------------------------------
+// The attention kernel already computed every scaled logit x = q.k * scale
+// (log2 domain) of the scored audio rows; with its final (max, sum) per head
+// a weight is exp2(x - max) / sum.  One thread per audio token of a sample
+// sums the weights over the flagged KV heads and their query heads, and
+// adds the total to the accumulator once (no atomics).  The validity rules
+// are those of attn_score_kernel, so both passes score the same rows.
+struct LogitScoreParams {
+  const float* xlog;       // [n_seg, G, max_audio]
+  const float* lse;        // [n_seg, G, 2] log2 domain
+  const int32_t* cu;       // [n_seg + 1]
+  const int64_t* base;     // [n_seg] or null
+  const int32_t* mask;     // [Hkv]
+  const int32_t* audio_s;  // [B]
+  const int32_t* audio_e;
+  const int32_t* acc_off;  // [B + 1]
+  float* acc;
+  int32_t* err;
+  int64_t kv_rows, acc_len, max_audio;
+  int32_t n_seg, G, Hkv;
+};
+
+static constexpr int kLogitThreads = 256;
+
+__global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(LogitScoreParams p) {
+  const int b = blockIdx.y;
+  const int a0 = p.audio_s[b], a1 = p.audio_e[b];
+  const int n_audio = a1 - a0;
+  const int64_t j = (int64_t)blockIdx.x * kLogitThreads + threadIdx.x;
+  if ((int64_t)blockIdx.x * kLogitThreads >= min((int64_t)n_audio, p.max_audio)) return;  // uniform
+  const bool valid = j < n_audio && j < p.max_audio;
+  const int64_t off = p.acc_off[b];
+  float total = 0.f;
+  for (int kv = 0; kv < p.Hkv; ++kv) {
+    if (!p.mask[kv]) continue;
+    const int s = b * p.Hkv + kv;
+    if (s >= p.n_seg) break;
+    const int64_t len = (int64_t)p.cu[s + 1] - p.cu[s];
+    const int64_t base = p.base ? p.base[s] : (int64_t)p.cu[s];
+    if (a0 < 0 || a1 > len || base < 0 || base + len > p.kv_rows || off + n_audio > p.acc_len) {
+      if (threadIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+      continue;  // uniform
+    }
+    float sc = 0.f;
+    for (int g = 0; g < p.G; ++g) {
+      const float m = p.lse[((int64_t)s * p.G + g) * 2];
+      const float inv = 1.f / p.lse[((int64_t)s * p.G + g) * 2 + 1];
+      const float x = valid ? p.xlog[((int64_t)s * p.G + g) * p.max_audio + j] : m;
+      sc += exp2f(x - m) * inv;
+    }
+    total += sc;
+  }
+  if (valid) p.acc[off + j] += total;
 }
 
 // ---------------------------------------------------------------------------
@@ -362,10 +413,17 @@ using namespace wnw;
 
 static int64_t up256(int64_t x) { return (x + 255) / 256 * 256; }
 
-extern "C" int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group, int64_t head_dim) {
+// Workspace of wnw_decode_attn_score: attention workspace, normalisers, then
+// (max_audio > 0) the logits of the scored audio rows.
+static int64_t score_logits_offset(int64_t attn_ws, int64_t n_seg, int64_t group) {
+  return attn_ws + up256(n_seg * group * 2 * 4);
+}
+
+extern "C" int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t group, int64_t head_dim,
+                                                         int64_t max_audio) {
   const int64_t a = wnw_decode_attn_workspace_bytes(n_seg, group, head_dim);
-  if (a < 0) return -1;
-  return a + up256(n_seg * group * 2 * 4);
+  if (a < 0 || max_audio < 0) return -1;
+  return score_logits_offset(a, n_seg, group) + up256(n_seg * group * max_audio * 4);
 }
 
 extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v, const int32_t* cu_k,
@@ -386,9 +444,46 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   WNW_CHECK_ARG(attn_ws >= 0 && workspace_bytes >= attn_ws + up256(n_seg * group * 8),
                 "workspace too small for attention + normalisers");
   float* lse = (float*)((char*)workspace + attn_ws);
+  // With room for them, the logits of the scored rows are kept by the
+  // attention kernel (when the streaming kernel runs) and the scoring pass
+  // reads 4 bytes per row and head instead of the K row.
+  const int64_t xoff = score_logits_offset(attn_ws, n_seg, group);
+  AttnLogits lg;
+  lg.xlog = (float*)((char*)workspace + xoff);
+  lg.mask = ca_kv_mask;
+  lg.audio_s = audio_starts;
+  lg.audio_e = audio_ends;
+  lg.max_audio = max_audio;
+  lg.hkv = (int32_t)num_kv_heads;
+  const bool room = max_audio > 0 && workspace_bytes >= xoff + n_seg * group * max_audio * 4;
+  int kept = 0;
   int rc = decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
-                            dtype, out, workspace, attn_ws, WNW_ATTN_AUTO, 0, lse, stream);
+                            dtype, out, workspace, attn_ws, WNW_ATTN_AUTO, 0, lse, room ? &lg : nullptr, &kept,
+                            stream);
   if (rc != WNW_OK || n_seg == 0 || max_audio == 0) return rc;
+  if (kept) {
+    LogitScoreParams lp;
+    lp.xlog = lg.xlog;
+    lp.lse = lse;
+    lp.cu = cu_k;
+    lp.base = seg_base;
+    lp.mask = ca_kv_mask;
+    lp.audio_s = audio_starts;
+    lp.audio_e = audio_ends;
+    lp.acc_off = score_offsets;
+    lp.acc = score_acc;
+    lp.err = device_error_word();
+    lp.kv_rows = kv_rows;
+    lp.acc_len = acc_len;
+    lp.max_audio = max_audio;
+    lp.n_seg = (int32_t)n_seg;
+    lp.G = (int32_t)group;
+    lp.Hkv = (int32_t)num_kv_heads;
+    const dim3 grid((unsigned)((max_audio + kLogitThreads - 1) / kLogitThreads), (unsigned)(n_seg / num_kv_heads));
+    hipLaunchKernelGGL(logit_score_kernel, grid, dim3(kLogitThreads), 0, (hipStream_t)stream, lp);
+    WNW_CHECK_HIP(hipGetLastError(), "logit score launch");
+    return WNW_OK;
+  }
   AttnScoreParams sp;
   sp.q = q;
   sp.k = k;

@@ -20,6 +20,27 @@ int32_t* device_error_word();
 // the query fails).
 int device_cus();
 
+// Logits of the scored (class-A) audio rows, kept by the streaming attention
+// kernel for the scoring pass: xlog[(s * G + g) * max_audio + t].
+struct AttnLogits {
+  float* xlog;
+  const int32_t* mask;     // [hkv] non-zero: KV head scored
+  const int32_t* audio_s;  // [n_seg / hkv], relative to the segments' starts
+  const int32_t* audio_e;
+  int64_t max_audio;
+  int32_t hkv;
+};
+
+// Shared by the public attention entry points; lse (optional) receives each
+// segment's final softmax (max, sum) in the log2 domain, [n_seg, G, 2].
+// logits (optional) is honoured by the streaming kernel only; *logits_kept
+// (optional) tells whether they were written.
+int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                     const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
+                     int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
+                     void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
+                     const AttnLogits* logits, int* logits_kept, void* stream);
+
 #define WNW_CHECK_ARG(cond, ...)       \
   do {                                 \
     if (!(cond)) {                     \

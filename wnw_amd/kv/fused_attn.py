@@ -28,12 +28,15 @@ class AttnWorkspace:
         self.buf: torch.Tensor | None = None
         self.cleared_for = -1  # n_seg of the layout whose counters are known to be zero
 
-    def get(self, n_seg: int, group: int, head_dim: int, score: bool = False) -> tuple[torch.Tensor, int]:
+    def get(self, n_seg: int, group: int, head_dim: int, score: bool = False,
+            max_audio: int = 0) -> tuple[torch.Tensor, int]:
         """Buffer and its size; ``score`` adds room for the softmax
-        normalisers of ``wnw_decode_attn_score``."""
-        query = _lib.lib().wnw_decode_attn_score_workspace_bytes if score else \
-            _lib.lib().wnw_decode_attn_workspace_bytes
-        need = int(query(n_seg, group, head_dim))
+        normalisers of ``wnw_decode_attn_score`` and, with ``max_audio`` > 0,
+        for the logits of the scored audio rows."""
+        if score:
+            need = int(_lib.lib().wnw_decode_attn_score_workspace_bytes(n_seg, group, head_dim, max_audio))
+        else:
+            need = int(_lib.lib().wnw_decode_attn_workspace_bytes(n_seg, group, head_dim))
         if need < 0:
             raise _lib.WnwError("bad workspace query")
         if self.buf is None or self.buf.numel() < need:
@@ -154,6 +157,7 @@ def q1_decode_attn_score(
     max_audio: int | None = None,
     out: torch.Tensor | None = None,
     workspace: AttnWorkspace | None = None,
+    keep_logits: bool = True,
 ) -> torch.Tensor:
     """Attention output [nseg, G, D] plus class-A score accumulation.
 
@@ -164,6 +168,9 @@ def q1_decode_attn_score(
     use the attention's own final softmax statistics.  ``max_audio`` (the
     largest ``audio_ends - audio_starts``) sizes the scoring grid; when it is
     not given it is read back from the device (one synchronisation).
+    ``keep_logits`` lets the attention kernel keep the logits of the scored
+    rows for the scoring pass (workspace of n_seg * G * max_audio floats);
+    without it the scoring pass reads the K rows again.
     """
     del block_n
     _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_accumulator,
@@ -192,7 +199,7 @@ def q1_decode_attn_score(
     rows = k_flat.shape[0] if total_rows is None else int(total_rows)
     _lib.ensure_init(q_flat.device)
     ws = workspace if workspace is not None else workspace_for(q_flat.device)
-    buf, nbytes = ws.get(nseg, g, d, score=True)
+    buf, nbytes = ws.get(nseg, g, d, score=True, max_audio=int(max_audio) if keep_logits else 0)
     _lib.check(_lib.lib().wnw_decode_attn_score(
         _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base), nseg, g, d, rows,
         k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(ca_kv_mask),
