@@ -205,7 +205,7 @@ int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
  * layout, seg_base NULL, always is); a violation sets WNW_DEVERR_ORDER and
  * a segment outside [0, kv_rows) sets WNW_DEVERR_BOUNDS and yields NaN.
  * total_rows (an upper bound of cu_k[n_seg]) is checked for sign only and
- * kept for signature stability.
+ * kept for signature stability.  q, k, v and out must be 16-byte aligned.
  */
 int wnw_decode_attn(const void* q, const void* k, const void* v,
                     const int32_t* cu_k, const int64_t* seg_base,

@@ -326,9 +326,8 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
       M = Mc;
     }
     const float inv = 1.f / L;
-    const int64_t e0 = s * GD + 4 * i4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) store_elem<T>(p.out, e0 + i, A[i] * inv);
+    const float o4[4] = {A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv};
+    store_quad<T>(p.out, s * GD + 4 * i4, o4);
     if (p.lse && (4 * i4) % D == 0) {
       gptr_w<float>(p.lse)[(s * G + g) * 2] = M;
       gptr_w<float>(p.lse)[(s * G + g) * 2 + 1] = L;
@@ -1581,8 +1580,9 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   WNW_CHECK_ARG(dtype == WNW_F32 || dtype == WNW_F16 || dtype == WNW_BF16, "bad dtype %d", dtype);
   WNW_CHECK_ARG(total_rows >= 0 && kv_rows >= 0, "negative row count");
   WNW_CHECK_ARG(kv_rows < (1ll << 40), "kv_rows too large");
-  WNW_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0,
-                "q, k and v must be 16-byte aligned");
+  WNW_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
+                    ((uintptr_t)out % 16) == 0,
+                "q, k, v and out must be 16-byte aligned");
   const WsLayout L = ws_layout(n_seg, group, head_dim);
   WNW_CHECK_ARG(workspace_bytes >= L.total, "workspace too small: %lld < %lld bytes",
                 (long long)workspace_bytes, (long long)L.total);

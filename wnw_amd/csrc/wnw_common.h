@@ -182,4 +182,22 @@ __device__ __forceinline__ void store_elem<f16_t>(void* base, int64_t i, float x
   gptr_w<uint16_t>(base)[i] = (uint16_t)f32_to_f16_bits(x);
 }
 
+__device__ __forceinline__ uint32_t half_bits(float x, bf16_t*) { return f32_to_bf16_bits(x); }
+__device__ __forceinline__ uint32_t half_bits(float x, f16_t*) { return f32_to_f16_bits(x); }
+
+// Elements i .. i + 3 (i a multiple of 4) of a T array at `base` = v, in one
+// store (rounded to nearest even).
+template <typename T>
+__device__ __forceinline__ void store_quad(void* base, int64_t i, const float (&v)[4]) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(T) == 4) {
+    *(WNW_GLOBAL u32x4*)(gptr_w<float>(base) + i) =
+        u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  } else {
+    auto cv = [](float x) -> uint32_t { return half_bits(x, (T*)nullptr); };
+    *(WNW_GLOBAL u32x2_t*)(gptr_w<uint16_t>(base) + i) =
+        u32x2_t{cv(v[0]) | (cv(v[1]) << 16), cv(v[2]) | (cv(v[3]) << 16)};
+  }
+}
+
 }  // namespace wnw
