@@ -785,6 +785,12 @@ struct StreamOps<bf16_t> {
   }
   __device__ static uint32_t from_f32(float x) { return f32_to_bf16_bits(x); }
   __device__ static float to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+  // two finite values, round to nearest even, in one v_cvt_pk_bf16_f32
+  __device__ static uint32_t pack2(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
+  }
 };
 template <>
 struct StreamOps<f16_t> {
@@ -803,6 +809,7 @@ struct StreamOps<f16_t> {
   }
   __device__ static uint32_t from_f32(float x) { return f32_to_f16_bits(x); }
   __device__ static float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
+  __device__ static uint32_t pack2(float a, float b) { return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16); }
 };
 
 template <int D>
@@ -1044,25 +1051,28 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
         if (r < st.nrows && t >= 0 && t < st.alen) xl[t] = x[i];
       }
     }
-    mx = fmaxf(mx, swap16(mx));
-    mx = fmaxf(mx, swap32(mx));
+    mx = max_x32(max_x16(mx));
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    // exp2 by v_exp_f32 directly: arguments are <= 0, and weights below
+    // 2^-126 (flushed to zero) are negligible beside the maximum's 1
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
-    uint32_t hb[4], lo[4];
+    float pv[4];
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float pv = exp2f(x[i] - m_new);
-      psum += pv;
-      hb[i] = Ops::from_f32(pv);
-      lo[i] = Ops::from_f32(pv - Ops::to_f32(hb[i]));
+      pv[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+      psum += pv[i];
     }
+    // P = hi + lo, each a 16-bit float: PV runs as two MFMAs with fp32-grade P
+    const uint32_t h01 = Ops::pack2(pv[0], pv[1]), h23 = Ops::pack2(pv[2], pv[3]);
+    const uint32_t l01 = Ops::pack2(pv[0] - Ops::to_f32(h01 & 0xffffu), pv[1] - Ops::to_f32(h01 >> 16));
+    const uint32_t l23 = Ops::pack2(pv[2] - Ops::to_f32(h23 & 0xffffu), pv[3] - Ops::to_f32(h23 >> 16));
     l_run = l_run * alpha + psum;
 #pragma unroll
     for (int t = 0; t < NTD; ++t) acc[t] *= alpha;
-    const uint64_t ph = (uint64_t)(hb[0] | (hb[1] << 16)) | ((uint64_t)(hb[2] | (hb[3] << 16)) << 32);
-    const uint64_t pl = (uint64_t)(lo[0] | (lo[1] << 16)) | ((uint64_t)(lo[2] | (lo[3] << 16)) << 32);
+    const uint64_t ph = (uint64_t)h01 | ((uint64_t)h23 << 32);
+    const uint64_t pl = (uint64_t)l01 | ((uint64_t)l23 << 32);
     __builtin_amdgcn_sched_barrier(0);
     if (has_next)
       wait_vmcnt<E>();
@@ -1085,8 +1095,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     }
     __builtin_amdgcn_sched_barrier(0);
     if (st.last) {
-      float l_tot = l_run + swap16(l_run);
-      l_tot += swap32(l_tot);
+      const float l_tot = sum_x32(sum_x16(l_run));
       if (st.whole) {  // the segment lies inside this wave's range: finish it
         if (lc < G) {
           WNW_GLOBAL uint16_t* o = gptr_w<uint16_t>(p.out) + ((int64_t)st.s * G + lc) * D;

@@ -73,10 +73,10 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 // fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = ((u >> 16) | 0x40u) & 0xffffu;
+  return (u & 0x7fffffffu) > 0x7f800000u ? qnan : rne;  // a select, not a branch
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -135,6 +135,27 @@ __device__ __forceinline__ float swap16(float x) {
 }
 // x from lane (lane ^ 32).
 __device__ __forceinline__ float swap32(float x) { return __shfl_xor(x, 32); }
+
+// Max / sum of x over lanes l and l ^ 16 (or l ^ 32) with the gfx950 row
+// swaps (v_permlane16_swap / v_permlane32_swap: VALU, no LDS round trip).
+// Each returns the pair {x[l], x[l ^ 16]} with the lower row's value first,
+// so both lanes of a pair compute the same result.
+__device__ __forceinline__ float max_x16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_x16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
