@@ -21,32 +21,33 @@ S_ATOL, S_RTOL = 1e-6, 1e-3
 
 
 def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_rows=None, kv_scale=1.0,
-                     keep_logits=True):
+                     keep_logits=True, dtype="bfloat16"):
     rng = np.random.default_rng(seed)
+    odt = oracle.DT_BF16 if dtype == "bfloat16" else oracle.DT_F16
     n = len(lens)
     B = n // H
     cu = cu_from_lens(lens)
     rows = int(cu[-1]) if pool_rows is None else pool_rows
-    q = rand_rows(rng, n * G, D, "bfloat16").reshape(n, G, D)
-    k = rand_rows(rng, rows, D, "bfloat16", kv_scale)
-    v = rand_rows(rng, rows, D, "bfloat16", kv_scale)
+    q = rand_rows(rng, n * G, D, dtype).reshape(n, G, D)
+    k = rand_rows(rng, rows, D, dtype, kv_scale)
+    v = rand_rows(rng, rows, D, dtype, kv_scale)
     offs = np.concatenate([[0], np.cumsum(np.array(a_e) - np.array(a_s))]).astype(np.int32)
     acc0 = rng.random(int(offs[-1])).astype(np.float32)
     scale = D ** -0.5
-    ref_out = oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=oracle.DT_BF16)
+    ref_out = oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=odt)
     ref_acc = oracle.attn_scores(q, k, cu, scale, mask, H, a_s, a_e, offs, acc0.astype(np.float64),
-                                 base=base, dtype=oracle.DT_BF16)
+                                 base=base, dtype=odt)
     t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
     acc = torch.from_numpy(acc0).to(dev)
     print(f"attn_score n_seg={n} H={H} G={G} D={D} mask={mask} seed={seed} keep_logits={keep_logits}", flush=True)
     out = fused_attn.q1_decode_attn_score(
-        to_torch(q, "bfloat16", dev), to_torch(k, "bfloat16", dev), to_torch(v, "bfloat16", dev), t(cu), scale,
+        to_torch(q, dtype, dev), to_torch(k, dtype, dev), to_torch(v, dtype, dev), t(cu), scale,
         t(mask), H, t(a_s), t(a_e), acc, t(offs),
         seg_base=None if base is None else t(base, torch.int64), max_audio=int(max(np.array(a_e) - np.array(a_s))),
         keep_logits=keep_logits)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
-    got_out = oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16)
+    got_out = oracle.to_f64(from_torch(out, dtype), odt)
     return got_out, ref_out, acc.cpu().numpy().astype(np.float64), ref_acc
 
 
@@ -57,6 +58,17 @@ def test_attn_score_small(keep_logits):
     lens = [40, 300, 17, 1000, 64, 2, 513, 90]  # B = 2, H = 4
     got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 4, 4, 128, [0, 1, 0, 1],
                                             [3, 0], [17, 2], seed=1, keep_logits=keep_logits)
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_f16_head_dim_64(keep_logits):
+    lens = [700, 30, 129, 64, 1, 333]  # B = 3, H = 2
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, 2, 4, 64, [1, 0], [0, 5, 0],
+                                            [650, 100, 1], seed=5, keep_logits=keep_logits, dtype="float16")
     ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
     assert ok, msg
     ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
