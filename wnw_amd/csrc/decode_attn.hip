@@ -878,8 +878,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   // swizzled by the row (K: chunk ^ (r % CH); V: chunk ^ 2 (r % 4)); rows past
   // nrows repeat the last row
   auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b) {
-    const T* src = (is_v ? vp : kp) + row0 * D;
-    const uint32_t dst = lds_w + b * 2 * SB + (is_v ? SB : 0);
+    // wave-uniform addresses, kept scalar (the load takes them in SGPRs)
+    const T* src = (const T*)uni((int64_t)(uintptr_t)((is_v ? vp : kp) + row0 * D));
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_w + b * 2 * SB + (is_v ? SB : 0));
+    nrows = uni((int32_t)nrows);
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int r = u * RPI + lane / CH;
@@ -988,11 +990,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   // ---- loads of one step into buffer b: K, q, V (E loads, in this order)
   auto issue = [&](const SStep& st, int b) {
     load_rows(false, st.row0, st.nrows, b);
-    const T* qs = (const T*)p.q + (int64_t)st.s * G * D;
+    const T* qs = (const T*)uni((int64_t)(uintptr_t)((const T*)p.q + (int64_t)st.s * G * D));
 #pragma unroll
     for (int u = 0; u < QD; ++u) {
       const int off = u * 1024 + lane * 16;
-      if (off < qbytes) dma_copy16(qs, (uint32_t)off, lds_q + st.qslot * qslot + u * 1024);
+      if (off < qbytes)
+        dma_copy16(qs, (uint32_t)off, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + u * 1024));
     }
     load_rows(true, st.row0, st.nrows, b);
   };
