@@ -154,6 +154,21 @@ def test_score_bad_audio_range_is_flagged():
 
 
 @pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_many_tiny_segments(keep_logits):
+    """8,192 segments alternating 1 and 0 rows: each workgroup's range spans
+    more than 64 segment indices, so the kernels read the offsets, flags and
+    audio ranges from memory instead of their LDS window."""
+    B, H = 4096, 2
+    lens = [1, 0] * B
+    got, ref, gacc, racc = _attn_score_case(torch.device("cuda", 0), lens, H, 4, 128, [1, 0], [0] * B, [1] * B,
+                                            seed=21, keep_logits=keep_logits)
+    ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+    assert ok, msg
+    ok, msg = allclose_report(gacc, racc, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("keep_logits", [True, False])
 def test_attn_score_bad_audio_range_is_flagged(keep_logits):
     """A flagged segment whose audio range ends past the segment sets the
     device error word; that sample's tokens are left untouched, the other
