@@ -199,24 +199,49 @@ __device__ __forceinline__ int rebuild_source(const RebuildDesc& d, int s, int64
   const WNW_GLOBAL int32_t* eoff = gptr<int32_t>(d.evict_offsets);
   const WNW_GLOBAL int32_t* est = gptr<int32_t>(d.evict_starts);
   const WNW_GLOBAL int32_t* een = gptr<int32_t>(d.evict_ends);
+  // every descriptor of the segment is read up front (independent loads)
   const int e0 = eoff[s];
   const int e1 = eoff[s + 1];
+  const int64_t ll = gptr<int32_t>(d.load_lens)[s];
+  const int64_t ls = gptr<int32_t>(d.load_starts)[s];
   const int ne = min(e1 - e0, d.max_evict);
   if (ne > 0 && (e0 < 0 || (int64_t)e0 + ne > d.n_evict)) return kNone;
+  // The evict ranges are read in batches of kEB whose loads are issued
+  // together (one memory round trip per batch, not per range); entries past
+  // ne read the last range again and count as empty.
+  constexpr int kEB = 8;
   int64_t kept = old_len;
-  for (int e = 0; e < ne; ++e) kept -= (int64_t)een[e0 + e] - est[e0 + e];
+  for (int b0 = 0; b0 < ne; b0 += kEB) {
+    int32_t es[kEB], ee[kEB];
+#pragma unroll
+    for (int u = 0; u < kEB; ++u) {
+      const int e = e0 + min(b0 + u, ne - 1);
+      es[u] = est[e];
+      ee[u] = een[e];
+    }
+#pragma unroll
+    for (int u = 0; u < kEB; ++u)
+      if (b0 + u < ne) kept -= (int64_t)ee[u] - es[u];
+  }
   if (i < kept) {
     int64_t rel = i;
-    for (int e = 0; e < ne; ++e) {
-      const int64_t es = est[e0 + e], ee = een[e0 + e];
-      if (rel >= es) rel += ee - es;
+    for (int b0 = 0; b0 < ne; b0 += kEB) {
+      int32_t es[kEB], ee[kEB];
+#pragma unroll
+      for (int u = 0; u < kEB; ++u) {
+        const int e = e0 + min(b0 + u, ne - 1);
+        es[u] = est[e];
+        ee[u] = een[e];
+      }
+#pragma unroll
+      for (int u = 0; u < kEB; ++u)
+        if (b0 + u < ne && rel >= es[u]) rel += (int64_t)ee[u] - es[u];
     }
     src = rel;
     return kOld;
   }
-  const int64_t ll = gptr<int32_t>(d.load_lens)[s];
   if (i < kept + ll) {
-    src = (int64_t)gptr<int32_t>(d.load_starts)[s] + (i - kept);
+    src = ls + (i - kept);
     return kLoad;
   }
   src = s;
