@@ -988,14 +988,18 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   };
 
   // ---- loads of one step into buffer b: K, q, V (E loads, in this order)
+  // q is loaded for the first step of a piece only (the later steps keep it
+  // in registers), so a step issues E loads with q and E - QD without.
   auto issue = [&](const SStep& st, int b) {
     load_rows(false, st.row0, st.nrows, b);
-    const T* qs = (const T*)uni((int64_t)(uintptr_t)((const T*)p.q + (int64_t)st.s * G * D));
+    if (st.first) {
+      const T* qs = (const T*)uni((int64_t)(uintptr_t)((const T*)p.q + (int64_t)st.s * G * D));
 #pragma unroll
-    for (int u = 0; u < QD; ++u) {
-      const int off = u * 1024 + lane * 16;
-      if (off < qbytes)
-        dma_copy16(qs, (uint32_t)off, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + u * 1024));
+      for (int u = 0; u < QD; ++u) {
+        const int off = u * 1024 + lane * 16;
+        if (off < qbytes)
+          dma_copy16(qs, (uint32_t)off, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + u * 1024));
+      }
     }
     load_rows(true, st.row0, st.nrows, b);
   };
@@ -1016,12 +1020,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   int64_t c_b = 0;
   u32x4 qb[NC];
 
-  auto process = [&](const SStep& st, int b, bool has_next) {
+  auto process = [&](const SStep& st, int b, bool has_next, bool next_first) {
     uint8_t* kbuf = wbuf + b * 2 * SB;
     uint8_t* vbuf = kbuf + SB;
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next)
+    // K (and q) of this step: its V and the next step may still load
+    if (has_next && next_first)
       wait_vmcnt<NI + E>();
+    else if (has_next)
+      wait_vmcnt<NI + E - QD>();
     else
       wait_vmcnt<NI>();
     __builtin_amdgcn_sched_barrier(0);
@@ -1077,8 +1084,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
     const uint64_t ph = (uint64_t)h01 | ((uint64_t)h23 << 32);
     const uint64_t pl = (uint64_t)l01 | ((uint64_t)l23 << 32);
     __builtin_amdgcn_sched_barrier(0);
-    if (has_next)
+    // V of this step: the next step may still load
+    if (has_next && next_first)
       wait_vmcnt<E>();
+    else if (has_next)
+      wait_vmcnt<E - QD>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_sched_barrier(0);
@@ -1145,11 +1155,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   bool hB = hA && gen(sB);
   if (hB) issue(sB, 1);
   while (hA) {
-    process(sA, 0, hB);
+    process(sA, 0, hB, hB && sB.first);
     hA = hB && gen(sA);  // the step after sB
     if (hA) issue(sA, 0);
     if (!hB) break;
-    process(sB, 1, hA);
+    process(sB, 1, hA, hA && sA.first);
     hB = hA && gen(sB);
     if (hB) issue(sB, 1);
     if (!hA) break;
