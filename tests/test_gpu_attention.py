@@ -276,3 +276,47 @@ def test_workspace_reuse_across_segment_counts(gpu):
             got, ref = _run_case(gpu, lens, 4, 64, "bfloat16", kernel=kernel, seed=n_seg, n_wg=0)
             ok, msg = allclose_report(got, ref, ATOL, RTOL)
             assert ok, f"n_seg={n_seg} {kernel}: {msg}"
+
+
+def _random_case(rng):
+    """One seeded random configuration: kernel, dtype, shape, ragged lengths
+    (empty, short, medium and long segments), dense or slack layout, split."""
+    kernel = rng.choice(["stream", "stream", "stream", "mfma", "valu"])
+    if kernel == "valu":
+        dtype = str(rng.choice(["bfloat16", "float16", "float32"]))
+        D = int(rng.choice([64, 128, 256]))
+        G = int(rng.integers(1, 17))
+    else:
+        dtype = str(rng.choice(["bfloat16", "float16"]))
+        D = int(rng.choice([64, 128]))
+        G = int(rng.integers(1, 9 if kernel == "stream" else 17))
+    n = int(rng.integers(1, 300))
+    kind = rng.random(n)
+    lens = np.where(kind < 0.1, 0, np.where(kind < 0.4, rng.integers(1, 20, n),
+                                            np.where(kind < 0.8, rng.integers(20, 600, n), rng.integers(600, 5000, n))))
+    lens = [int(x) for x in lens]
+    base = pool = None
+    if rng.random() < 0.5:  # slack layout: gaps of garbage rows between the segments
+        gaps = rng.integers(0, 40, n)
+        base = np.zeros(n, np.int64)
+        pos = int(rng.integers(0, 16))
+        for s in range(n):
+            base[s] = pos
+            pos += lens[s] + int(gaps[s])
+        pool = pos + int(rng.integers(0, 16))
+    n_wg = 0 if rng.random() < 0.5 else int(rng.integers(1, 600))
+    return dict(lens=lens, G=G, D=D, dtype=dtype, kernel=str(kernel), n_wg=n_wg, base=base, pool_rows=pool)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_configurations(gpu, seed):
+    """A seeded sweep over kernels, dtypes, head sizes, groups, ragged
+    segment lengths, layouts and workgroup counts, each against the oracle."""
+    c = _random_case(np.random.default_rng(1000 + seed))
+    if sum(c["lens"]) == 0 and c["base"] is None:
+        c["lens"][0] = 1
+    got, ref = _run_case(gpu, c["lens"], c["G"], c["D"], c["dtype"], kernel=c["kernel"], n_wg=c["n_wg"],
+                         seed=seed, base=c["base"], pool_rows=c["pool_rows"])
+    atol, rtol = _tol(c["dtype"])
+    ok, msg = allclose_report(got, ref, atol, rtol)
+    assert ok, f"{c['kernel']} {c['dtype']} D={c['D']} G={c['G']} n_seg={len(c['lens'])} n_wg={c['n_wg']}: {msg}"
