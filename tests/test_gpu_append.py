@@ -162,3 +162,45 @@ def test_append_inplace_capacity_is_enforced(gpu):
     assert _lib.device_error() & _lib.DEVERR_CAPACITY
     assert torch.all(k[4] == 0)  # not written past capacity
     assert torch.all(k[12] == 1)  # segment 1 appended
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_rebuild_random_sweep(gpu, seed):
+    """Seeded sweep: up to 30 evict ranges per segment (several batches of
+    the kernel's range reads), MAX_EVICT truncation, head sizes, dtypes."""
+    rng = np.random.default_rng(500 + seed)
+    dtype = str(rng.choice(["bfloat16", "float16", "float32"]))
+    D = int(rng.choice([64, 128, 256]))
+    n = int(rng.integers(1, 200))
+    pool = int(rng.integers(0, 900))
+    lens = rng.integers(0, 800, size=n)
+    ls, ll, eo, es, ee, nl = rand_rebuild_descriptors(rng, lens, pool, max_ranges=int(rng.choice([3, 12, 30])),
+                                                      p_change=0.8)
+    widest = int(np.max(np.diff(eo))) if n else 0
+    # the reference's MAX_EVICT: the widest segment's count, or fewer (later ranges ignored)
+    max_evict = max(1, widest if rng.random() < 0.5 else int(rng.integers(1, max(2, widest + 1))))
+    if max_evict < widest:
+        # with ranges ignored, a segment keeps more rows: the reference's new length follows kept_len
+        kept = []
+        for s in range(n):
+            k = min(int(eo[s + 1] - eo[s]), max_evict)
+            kept.append(int(lens[s]) - int(np.sum(ee[eo[s]:eo[s] + k] - es[eo[s]:eo[s] + k])))
+        nl = np.array([kept[s] + int(ll[s]) + 1 for s in range(n)], np.int32)
+    old_cu, new_cu = cu_from_lens(lens), cu_from_lens(nl)
+    T = int(old_cu[-1])
+    ok, ov = rand_rows(rng, T, D, dtype), rand_rows(rng, T, D, dtype)
+    nk, nv = rand_rows(rng, n, D, dtype), rand_rows(rng, n, D, dtype)
+    lk, lv = rand_rows(rng, pool, D, dtype), rand_rows(rng, pool, D, dtype)
+    code = DTYPE_CODES[dtype]
+    rk, rv = oracle.rebuild_append_kv(ok, ov, nk, nv, lk, lv, old_cu, new_cu, ls, ll, eo, es, ee, max_evict,
+                                      dtype=code)
+    print(f"rebuild sweep seed={seed} {dtype} D={D} n={n} rows={T}->{new_cu[-1]} ranges={len(es)} "
+          f"widest={widest} max_evict={max_evict}", flush=True)
+    T_ = lambda a: to_torch(a, dtype, gpu)  # noqa: E731
+    gk, gv = wnw_kernels.rebuild_append_kv(T_(ok), T_(ov), T_(nk), T_(nv), T_(lk), T_(lv), _t(old_cu, gpu),
+                                           _t(new_cu, gpu), _t(ls, gpu), _t(ll, gpu), _t(eo, gpu), _t(es, gpu),
+                                           _t(ee, gpu), max_evict)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    np.testing.assert_array_equal(from_torch(gk, dtype), rk)
+    np.testing.assert_array_equal(from_torch(gv, dtype), rv)
