@@ -268,9 +268,6 @@ __device__ __forceinline__ void st_agent2(float* p, float a, float b) {
   const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
   __hip_atomic_store(gptr_w<uint64_t>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint64_t ld_agent2(const float* p) {
-  return __hip_atomic_load(gptr_w<uint64_t>(const_cast<float*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // s_waitcnt vmcnt(0): every vector memory access of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // s_waitcnt vmcnt(n) (expcnt and lgkmcnt not waited on), n < 64.
@@ -283,45 +280,57 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Last-arriver merge of the np partials of one segment (slots s0 ..
 // s0 + np - 1) into the output, by threads t = 0 .. nt - 1.  Every thread
 // owns 4 consecutive elements of one head and reads, for a chunk of partials
-// at a time, their (m, l) pairs and its accumulator quad with agent-coherent
-// loads: one memory round trip per chunk, no LDS and no barriers.  Chunks
-// are folded in slot order with the usual max rescaling, so the result is
-// deterministic.
+// at a time, their (m, l) pairs and its accumulator quad: one memory round
+// trip per chunk, no LDS and no barriers.  The reads are buffer loads with
+// the sc1 policy (the agent-coherent form of a load on gfx950), one 16-byte
+// and one 8-byte load per partial at a scalar offset from the segment's
+// first slot.  Chunks are folded in slot order with the usual max
+// rescaling, so the result is deterministic.
 template <typename T>
 __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64_t s0, int np, int64_t s, int t,
                                                int nt) {
-  constexpr int QC = 16;  // partials per round trip
+  // the segment and its slots are wave-uniform: scalar, so the buffer
+  // descriptors below live in SGPRs
+  s0 = uni(s0);
+  np = uni(np);
+  s = uni(s);
+  constexpr int QC = 16;             // partials per round trip
+  constexpr int kSc1 = 16;           // buffer cache policy: sc1
+  constexpr int kRsrc3 = 0x00020000;  // buffer descriptor word 3 (raw 32-bit data) on gfx9
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   const int G = p.G;
   const int GD = G * D;
   const int GD4 = GD / 4;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(p.part_acc + s0 * GD, 0, np * GD * 4, kRsrc3);
+  const __amdgpu_buffer_rsrc_t rm =
+      __builtin_amdgcn_make_buffer_rsrc(p.part_ml + s0 * G * 2, 0, np * G * 8, kRsrc3);
   for (int i4 = t; i4 < GD4; i4 += nt) {
     const int g = (4 * i4) / D;
     float M = kNegBig, L = 0.f;
     f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int q0 = 0; q0 < np; q0 += QC) {
-      uint64_t ml[QC], a01[QC], a23[QC];
+      f32x4 a[QC];
+      u32x2 ml[QC];
 #pragma unroll
       for (int k = 0; k < QC; ++k) {
-        const int64_t slot = s0 + min(q0 + k, np - 1);  // past np: a repeat, masked below
-        ml[k] = ld_agent2(p.part_ml + (slot * G + g) * 2);
-        a01[k] = ld_agent2(p.part_acc + slot * GD + 4 * i4);
-        a23[k] = ld_agent2(p.part_acc + slot * GD + 4 * i4 + 2);
+        const int kk = min(q0 + k, np - 1);  // past np: a repeat, masked below
+        a[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, i4 * 16, kk * GD * 4, kSc1));
+        ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rm, g * 8, kk * G * 8, kSc1);
       }
       float Mc = M;
 #pragma unroll
       for (int k = 0; k < QC; ++k)
-        if (q0 + k < np) Mc = fmaxf(Mc, __uint_as_float((uint32_t)ml[k]));
-      const float so = exp2f(M - Mc);
+        if (q0 + k < np) Mc = fmaxf(Mc, __uint_as_float(ml[k].x));
+      const float so = __builtin_amdgcn_exp2f(M - Mc);
       L *= so;
       A *= so;
 #pragma unroll
       for (int k = 0; k < QC; ++k) {
         if (q0 + k >= np) continue;
-        const float wk = exp2f(__uint_as_float((uint32_t)ml[k]) - Mc);
-        L += __uint_as_float((uint32_t)(ml[k] >> 32)) * wk;
-        A += f32x4{__uint_as_float((uint32_t)a01[k]), __uint_as_float((uint32_t)(a01[k] >> 32)),
-                   __uint_as_float((uint32_t)a23[k]), __uint_as_float((uint32_t)(a23[k] >> 32))} *
-             wk;
+        const float wk = __builtin_amdgcn_exp2f(__uint_as_float(ml[k].x) - Mc);
+        L += __uint_as_float(ml[k].y) * wk;
+        A += a[k] * wk;
       }
       M = Mc;
     }
@@ -1194,108 +1203,111 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   put(2 * w + 1, c_s, c_b, c_len, m_run, l_run, acc);
   __syncthreads();
   // Slot headers: lane i reads header i % NS (one LDS read for all of
-  // them), then every header is broadcast from its lane into scalars.
-  // Slots follow the row order, and segments are disjoint and ordered, so
-  // the slots of one segment are consecutive (empty slots aside); a slot
-  // leads when no earlier slot holds its segment.
+  // them).  Slots follow the row order, and segments are disjoint and
+  // ordered, so the segment numbers of the non-empty slots never decrease:
+  // a slot leads its segment when its number exceeds every earlier slot's,
+  // and only the segments of the first and the last non-empty slot can
+  // cross the workgroup's range boundaries (those become partials for the
+  // last-arriver combine; every other segment is written out).
   constexpr int NS = 2 * NW;
   static_assert(NS <= 16, "merge slot headers");
   typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
   const i32x4 hv = *(const i32x4*)sl.hdr[lane % NS];
-  int32_t ss[NS], sn[NS];
-  int64_t sb[NS];
+  int32_t ss[NS];
 #pragma unroll
-  for (int i = 0; i < NS; ++i) {
-    ss[i] = __builtin_amdgcn_readlane(hv.x, i);
-    sn[i] = __builtin_amdgcn_readlane(hv.y, i);
-    sb[i] = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hv.w, i) << 32) |
-                      (uint32_t)__builtin_amdgcn_readlane(hv.z, i));
-  }
-  // Per leader: the slots of its segment (bit mask).  At most two segments
-  // cross the workgroup's range boundaries (segments are disjoint); those
-  // become partials for the last-arriver combine, the others are written.
+  for (int i = 0; i < NS; ++i) ss[i] = __builtin_amdgcn_readlane(hv.x, i);
   uint32_t lead = 0;
+  {
+    int32_t top = -1;
 #pragma unroll
-  for (int a = 0; a < NS; ++a) {
-    bool dup = ss[a] < 0;
-#pragma unroll
-    for (int j = 0; j < a; ++j) dup = dup || ss[j] == ss[a];
-    if (!dup) lead |= 1u << a;
+    for (int i = 0; i < NS; ++i) {
+      if (ss[i] > top) lead |= 1u << i;
+      top = max(top, ss[i]);
+    }
   }
   int32_t ps0 = -1, ps1 = -1, pl0 = 0, pl1 = 0;
   int64_t pb0 = 0, pb1 = 0;
-  const int GD = G * D;
-  const int GD4 = GD / 4;
-  while (lead) {
-    const int a = __builtin_ctz(lead);
-    lead &= lead - 1;
-    int32_t sa = -1, na = 0;
-    int64_t ba = 0;
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-      if (j == a) {
-        sa = ss[j];
-        na = sn[j];
-        ba = sb[j];
-      }
-    uint32_t memb = 0;
-#pragma unroll
-    for (int j = 0; j < NS; ++j) memb |= (ss[j] == sa ? 1u : 0u) << j;
-    const bool inside = ba >= B0 && ba + na <= B1;
-    const int64_t pslot = (int64_t)blockIdx.x + sa;
-    // one thread per 4 consecutive elements of one head.  Every slot is
-    // read (no branches between the loads, so they share one LDS round
-    // trip); selects drop the other segments' slots, whatever they hold.
-    for (int i4 = tid; i4 < GD4; i4 += NT) {
-      const int g = (4 * i4) / D;
-      float mv[NS], lv[NS];
-      f32x4 av[NS];
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        const float* ml = (const float*)slot_of(j);
-        mv[j] = ml[g];
-        lv[j] = ml[kMaxGroupS + g];
-        av[j] = *(const f32x4*)((const float*)(slot_of(j) + 2 * kMaxGroupS * 4) + g * G_::DP + (4 * i4 - g * D));
-      }
-      float M = kNegBig;
-#pragma unroll
-      for (int j = 0; j < NS; ++j) M = fmaxf(M, ((memb >> j) & 1) ? mv[j] : kNegBig);
-      float L = 0.f;
-      f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        const bool in = (memb >> j) & 1;
-        const float sc = in ? exp2f(mv[j] - M) : 0.f;
-        L += in ? lv[j] * sc : 0.f;
-        A += in ? av[j] * sc : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      const bool lead_elem = (4 * i4) % D == 0;
-      if (inside) {
-        const float inv = 1.f / L;
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const uint32_t w0 = Ops::from_f32(A[0] * inv) | (Ops::from_f32(A[1] * inv) << 16);
-        const uint32_t w1 = Ops::from_f32(A[2] * inv) | (Ops::from_f32(A[3] * inv) << 16);
-        *((WNW_GLOBAL u32x2*)gptr_w<uint16_t>(p.out) + ((int64_t)sa * GD4 + i4)) = u32x2{w0, w1};
-        if (p.lse && lead_elem) {
-          gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2] = M;
-          gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2 + 1] = L;
-        }
+  if (lead) {
+    const uint32_t used = (uint32_t)__ballot(lane < NS && hv.x >= 0);
+    const int jf = __builtin_ctz(used), jl = 31 - __builtin_clz(used);
+    auto base_of = [&](int j) {
+      return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hv.w, j) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane(hv.z, j));
+    };
+    const int64_t bf = base_of(jf), bl = base_of(jl);
+    const int32_t nf = __builtin_amdgcn_readlane(hv.y, jf), nl = __builtin_amdgcn_readlane(hv.y, jl);
+    const int32_t sf = __builtin_amdgcn_readlane(hv.x, jf), sg = __builtin_amdgcn_readlane(hv.x, jl);
+    if (bf < B0 || bf + nf > B1) {
+      ps0 = sf;
+      pb0 = bf;
+      pl0 = nf;
+    }
+    if (sg != sf && bl + nl > B1) {
+      if (ps0 < 0) {
+        ps0 = sg;
+        pb0 = bl;
+        pl0 = nl;
       } else {
-        st_agent2(p.part_acc + pslot * GD + 4 * i4, A[0], A[1]);
-        st_agent2(p.part_acc + pslot * GD + 4 * i4 + 2, A[2], A[3]);
-        if (lead_elem) st_agent2(p.part_ml + (pslot * G + g) * 2, M, L);
+        ps1 = sg;
+        pb1 = bl;
+        pl1 = nl;
       }
     }
-    if (!inside) {
-      if (ps0 < 0) {
-        ps0 = sa;
-        pb0 = ba;
-        pl0 = na;
-      } else {
-        ps1 = sa;
-        pb1 = ba;
-        pl1 = na;
+  }
+  const int GD = G * D;
+  const int GD4 = GD / 4;
+  // Task t = (leader t / GD4, quad t % GD4) over all threads: one thread per
+  // 4 consecutive elements of one head of one segment.  Every slot is read
+  // (no branches between the loads, so they share one LDS round trip);
+  // selects drop the other segments' slots, whatever they hold.
+  const int n_lead = __builtin_popcount(lead);
+  for (int t = tid; t < n_lead * GD4; t += NT) {
+    const int li = t / GD4, i4 = t - li * GD4;
+    uint32_t lm = lead;
+    for (int r = 0; r < li; ++r) lm &= lm - 1;
+    const int a = __builtin_ctz(lm);
+    const i32x4 ha = *(const i32x4*)sl.hdr[a];
+    const int32_t sa = ha.x, na = ha.y;
+    const int64_t ba = (int64_t)(((uint64_t)(uint32_t)ha.w << 32) | (uint32_t)ha.z);
+    const bool inside = ba >= B0 && ba + na <= B1;
+    const int g = (4 * i4) / D;
+    float mv[NS], lv[NS];
+    f32x4 av[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const float* ml = (const float*)slot_of(j);
+      mv[j] = ml[g];
+      lv[j] = ml[kMaxGroupS + g];
+      av[j] = *(const f32x4*)((const float*)(slot_of(j) + 2 * kMaxGroupS * 4) + g * G_::DP + (4 * i4 - g * D));
+    }
+    float M = kNegBig;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) M = fmaxf(M, ss[j] == sa ? mv[j] : kNegBig);
+    float L = 0.f;
+    f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const bool in = ss[j] == sa;
+      const float sc = in ? __builtin_amdgcn_exp2f(mv[j] - M) : 0.f;
+      L += in ? lv[j] * sc : 0.f;
+      A += in ? av[j] * sc : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bool lead_elem = (4 * i4) % D == 0;
+    if (inside) {
+      const float inv = 1.f / L;
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      const uint32_t w0 = Ops::from_f32(A[0] * inv) | (Ops::from_f32(A[1] * inv) << 16);
+      const uint32_t w1 = Ops::from_f32(A[2] * inv) | (Ops::from_f32(A[3] * inv) << 16);
+      *((WNW_GLOBAL u32x2*)gptr_w<uint16_t>(p.out) + ((int64_t)sa * GD4 + i4)) = u32x2{w0, w1};
+      if (p.lse && lead_elem) {
+        gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2] = M;
+        gptr_w<float>(p.lse)[((int64_t)sa * G + g) * 2 + 1] = L;
       }
+    } else {
+      const int64_t pslot = (int64_t)blockIdx.x + sa;
+      st_agent2(p.part_acc + pslot * GD + 4 * i4, A[0], A[1]);
+      st_agent2(p.part_acc + pslot * GD + 4 * i4 + 2, A[2], A[3]);
+      if (lead_elem) st_agent2(p.part_ml + (pslot * G + g) * 2, M, L);
     }
   }
   // piece counts of the partial segments, worked out while the stores drain
