@@ -236,6 +236,36 @@ def test_many_tiny_segments(gpu, kernel):
     assert ok, msg
 
 
+@pytest.mark.parametrize("kernel", ["stream", "mfma", "valu"])
+@pytest.mark.parametrize("n_wg", [1, 3, 64])
+def test_nonfinite_rows_stay_in_their_segment(gpu, kernel, n_wg):
+    """A NaN in one segment's K and an Inf in its V leave every other segment
+    exact: with few workgroups, several segments share one workgroup's merge
+    slots and combine, so any leak across segments would show here."""
+    lens = [40, 300, 17, 129, 64, 5, 700, 33]
+    bad = 3
+    G, D, dtype = 4, 128, "bfloat16"
+    rng = np.random.default_rng(5)
+    cu = cu_from_lens(lens)
+    T = int(cu[-1])
+    q = rand_rows(rng, len(lens) * G, D, dtype).reshape(len(lens), G, D)
+    k = rand_rows(rng, T, D, dtype)
+    v = rand_rows(rng, T, D, dtype)
+    k[cu[bad] + 7, 0] = 0x7FC0  # NaN
+    v[cu[bad] + 2, 5] = 0x7F80  # +Inf
+    ref = oracle.decode_attn(q, k, v, cu, D ** -0.5, dtype=DTYPE_CODES[dtype])
+    print(f"case nonfinite kernel={kernel} n_wg={n_wg}", flush=True)
+    out = fused_attn.decode_attn(to_torch(q, dtype, gpu), to_torch(k, dtype, gpu), to_torch(v, dtype, gpu),
+                                 torch.from_numpy(cu).to(gpu), D ** -0.5, total_rows=T, kernel=kernel, n_wg=n_wg)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    got = oracle.to_f64(from_torch(out, dtype), DTYPE_CODES[dtype])
+    keep = [s for s in range(len(lens)) if s != bad]
+    ok, msg = allclose_report(got[keep], ref[keep], ATOL, RTOL)
+    assert ok, msg
+    assert not np.all(np.isfinite(got[bad]))
+
+
 @pytest.mark.parametrize("lens", [[17], [16, 16, 16, 16], [15, 1, 33, 64, 5], [1000, 1, 1, 1000]])
 def test_stream_step_boundaries(gpu, lens):
     """Pieces ending mid-step, single-row pieces and exact multiples of the 16-row step."""
