@@ -899,13 +899,39 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
       dma_copy16(src, (uint32_t)(rr * RB + (((lane % CH) ^ sw) * 16)), dst + u * 1024);
     }
   };
-  schedule<T, NT, XL>(p, D, sl);
-  if (sl.s_first > sl.s_last) return;
-  const int64_t R = uni(sl.R);
-  const int64_t B0 = uni(sl.B0), B1 = uni(sl.B1);
+  // Up to 64 segments ("direct"): every wave reads the segment table itself,
+  // one lane per segment, and issues its first steps as soon as it arrives;
+  // the workgroup's checks of the table (and the outputs of empty or
+  // invalid segments) follow once those loads are out.  More segments: the
+  // workgroup pass of schedule() first, with its LDS cache of the bounds.
+  const bool direct = p.n_seg <= 64;
+  int64_t R, B0, B1;
+  int s_first, s_last;
+  if (direct) {
+    R = p.kv_rows;
+    const int64_t P = effective_wgs(R);
+    const bool active = (int64_t)blockIdx.x < P;
+    B0 = active ? range_start(blockIdx.x, R, P) : 0;
+    B1 = active ? range_start(blockIdx.x + 1, R, P) : 0;
+    s_first = 0;
+    s_last = p.n_seg - 1;
+    if (tid == 0) {  // read by the merge and the hand-off, after barriers
+      sl.R = R;
+      sl.P = (int32_t)P;
+      sl.B0 = B0;
+      sl.B1 = B1;
+    }
+  } else {
+    schedule<T, NT, XL>(p, D, sl);
+    if (sl.s_first > sl.s_last) return;
+    R = uni(sl.R);
+    B0 = uni(sl.B0);
+    B1 = uni(sl.B1);
+    s_first = uni(sl.s_first);
+    s_last = uni(sl.s_last);
+  }
   const int64_t W0 = B0 + (B1 - B0) * w / NW, W1 = B0 + (B1 - B0) * (w + 1) / NW;
-  const int s_first = uni(sl.s_first), s_last = uni(sl.s_last);
-  const bool in_ring = (s_last - s_first) < kRing;
+  const bool in_ring = !direct && (s_last - s_first) < kRing;
 
   // ---- segment walk: a window of 64 segments, one per lane; the mask holds
   // the valid ones overlapping [W0, W1) that are not taken yet.
@@ -1163,6 +1189,36 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
   if (hA) issue(sA, 0);
   bool hB = hA && gen(sB);
   if (hB) issue(sB, 1);
+  // direct: the checks of schedule() from the table window in registers
+  // (lane i holds segment i; no new loads, which would wait behind the
+  // steps just issued).  Wave 0 of every workgroup; the outputs of empty
+  // and invalid segments are written by workgroup i % grid.
+  if (direct && w == 0) {
+    // base of segment lane + 1 (read with every lane active)
+    const uint32_t nlo = __shfl_down((uint32_t)lb, 1), nhi = __shfl_down((uint32_t)((uint64_t)lb >> 32), 1);
+    const int64_t nb = (int64_t)(((uint64_t)nhi << 32) | nlo);
+    const int si = lane;
+    int64_t len = si < p.n_seg ? llen : 0;
+    if (len < 0) {  // corrupt offsets: treated as an empty segment
+      raise_device_error(p.err, WNW_DEVERR_ORDER);
+      len = 0;
+    }
+    if (p.base && si + 1 < p.n_seg && lb + len > nb) raise_device_error(p.err, WNW_DEVERR_ORDER);
+    if (si < p.n_seg && (len == 0 || lb < 0 || lb + len > R)) {
+      if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+      if ((si % (int)gridDim.x) == (int)blockIdx.x) {
+        const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
+        for (int e = 0; e < G * D; ++e) store_elem<T>(p.out, (int64_t)si * G * D + e, fill);
+        if (p.lse) {
+          WNW_GLOBAL float* ls = gptr_w<float>(p.lse) + (int64_t)si * G * 2;
+          for (int g = 0; g < G; ++g) {
+            ls[2 * g] = len == 0 ? kNegBig : fill;
+            ls[2 * g + 1] = len == 0 ? 0.f : fill;
+          }
+        }
+      }
+    }
+  }
   while (hA) {
     process(sA, 0, hB, hB && sB.first);
     hA = hB && gen(sA);  // the step after sB
