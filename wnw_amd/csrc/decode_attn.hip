@@ -855,7 +855,22 @@ struct SStep {
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
 template <typename T, int D, int NW, int QD, bool XL>
-__global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(AttnParams p) {
+// The fields read first lead the argument list as scalars: the build
+// preloads the first 16 argument dwords into SGPRs at dispatch
+// (-amdgpu-kernarg-preload-count), so the segment table and the first steps
+// are addressed without a kernel-argument load; aggregates are not preloaded.
+__global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_arg, const void* k_arg, const void* v_arg,
+                                                               const int32_t* cu_arg, const int64_t* base_arg,
+                                                               int64_t rows_arg, int32_t nseg_arg, int32_t g_arg,
+                                                               AttnParams p) {
+  p.q = q_arg;
+  p.k = k_arg;
+  p.v = v_arg;
+  p.cu = cu_arg;
+  p.base = base_arg;
+  p.kv_rows = rows_arg;
+  p.n_seg = nseg_arg;
+  p.G = g_arg;
   using G_ = StreamGeom<D>;
   using Ops = StreamOps<T>;
   constexpr int NT = NW * 64;
@@ -1594,7 +1609,8 @@ static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t 
                                    hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes(D, kNW, 2048));
   });
   if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap);
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap.q,
+                     ap.k, ap.v, ap.cu, ap.base, ap.kv_rows, ap.n_seg, ap.G, ap);
   return hipGetLastError();
 }
 
