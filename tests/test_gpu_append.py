@@ -164,6 +164,33 @@ def test_append_inplace_capacity_is_enforced(gpu):
     assert torch.all(k[12] == 1)  # segment 1 appended
 
 
+def test_rebuild_beyond_infinity_cache_bit_exact(gpu):
+    """A layer whose K and V output exceeds 256 MB (~600 K rows of bf16,
+    d 128) takes the non-temporal copies: still bit-exact."""
+    rng = np.random.default_rng(77)
+    n, D, dtype = 512, 128, "bfloat16"
+    lens = rng.integers(1200, 1600, size=n)
+    pool = 3000
+    ls, ll, eo, es, ee, nl = rand_rebuild_descriptors(rng, lens, pool, max_ranges=3)
+    old_cu, new_cu = cu_from_lens(lens), cu_from_lens(nl)
+    T = int(old_cu[-1])
+    assert int(new_cu[-1]) * D * 2 * 2 > (256 << 20)
+    bits = lambda rows: rng.integers(0, 1 << 16, size=(rows, D), dtype=np.uint16)  # noqa: E731
+    ok, ov, nk, nv, lk, lv = bits(T), bits(T), bits(n), bits(n), bits(pool), bits(pool)
+    max_evict = int(np.max(np.diff(eo)))
+    rk, rv = oracle.rebuild_append_kv(ok, ov, nk, nv, lk, lv, old_cu, new_cu, ls, ll, eo, es, ee, max_evict,
+                                      dtype=DTYPE_CODES[dtype])
+    print(f"rebuild large rows={T}->{new_cu[-1]} ranges={len(es)}", flush=True)
+    T_ = lambda a: to_torch(a, dtype, gpu)  # noqa: E731
+    gk, gv = wnw_kernels.rebuild_append_kv(T_(ok), T_(ov), T_(nk), T_(nv), T_(lk), T_(lv), _t(old_cu, gpu),
+                                           _t(new_cu, gpu), _t(ls, gpu), _t(ll, gpu), _t(eo, gpu), _t(es, gpu),
+                                           _t(ee, gpu), max_evict)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    np.testing.assert_array_equal(from_torch(gk, dtype), rk)
+    np.testing.assert_array_equal(from_torch(gv, dtype), rv)
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_rebuild_random_sweep(gpu, seed):
     """Seeded sweep: up to 30 evict ranges per segment (several batches of
