@@ -25,8 +25,9 @@ Reported:
                     layout, per layer: class-B segments drop their oldest
                     window row, every segment gets a new row; µs per layer
                     and TB/s of rows moved.
-* cpu_baseline   -- the float64 C oracle (1 core) on a bounded sample of the
-                    same layers.
+* cpu_baseline   -- the reference's decode layer-step restated in PyTorch
+                    (torch.cat append + per-segment float32 attention) on the
+                    host's cores, on a bounded sample of the same layers.
 
 ``--copy-calibration`` only runs a plain 256 MiB device-to-device copy three
 times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes).
@@ -113,6 +114,16 @@ class LayerState:
 
     def reset(self):
         self.cu[0].copy_(self.cu_init)
+
+    def dense_host(self):
+        """The logical rows of every segment under cu[0], gathered into the
+        reference's dense layout on the host: (k, v, cu)."""
+        import torch
+
+        cu = self.cu[0].cpu()
+        lens = (cu[1:] - cu[:-1]).to(torch.int64)
+        idx = torch.cat([self.base[s].cpu() + torch.arange(int(lens[s])) for s in range(self.n)])
+        return self.k.cpu()[idx], self.v.cpu()[idx], cu
 
 
 def main():
@@ -286,7 +297,7 @@ def main():
     # ---- CPU baseline: float64 C oracle on a bounded sample ---------------
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, layers, rows_attn, scale, args.cpu_sample_layers)
+        cpu = cpu_baseline(cfg, layers, scale, args.cpu_sample_layers)
 
     line = {
         "metric": METRIC,
@@ -388,34 +399,60 @@ def traffic_from_profiles(workload: str):
         return None
 
 
-def cpu_baseline(cfg, layers, rows_attn, scale, sample_layers: int):
-    """Float64 C oracle (single core) on a bounded sample of the workload."""
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: os.cpu_count(), capped by the
+    process's CPU affinity and by OMP_NUM_THREADS when that is set (the GPU
+    box gives one GPU's job a share of its cores)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except (AttributeError, OSError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_baseline(cfg, layers, scale, sample_layers: int, budget_s: float = 15.0):
+    """The reference's decode layer-step in PyTorch on the host's cores
+    (``oracle/torch_cpu.py``): the append of the step's row to every segment
+    (``torch.cat``, out of place) and per-segment float32 attention, on a
+    bounded sample of the workload's layers (the dense logical rows of each
+    layer, copied to the host before timing)."""
     import numpy as np
     import torch
 
-    import oracle
+    from oracle import torch_cpu
 
+    threads = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
     D, G = cfg.head_dim, cfg.group
     elapsed, done, bytes_done = 0.0, 0, 0
-    budget_s = 15.0
     limit = sample_layers if sample_layers > 0 else len(layers)
-    for li, st in enumerate(layers[:limit]):
-        cu = st.cu[0].cpu().numpy()
-        base = st.base.cpu().numpy()
-        k = st.k.cpu().view(torch.int16).numpy().view(np.uint16)
-        v = st.v.cpu().view(torch.int16).numpy().view(np.uint16)
-        q = st.q.cpu().view(torch.int16).numpy().view(np.uint16)
-        t0 = time.perf_counter()
-        oracle.decode_attn(q, k, v, cu, scale, base=base, dtype=oracle.DT_BF16)
-        elapsed += time.perf_counter() - t0
-        done += 1
-        bytes_done += rows_attn[li] * D * 2 * 2 + 2 * cfg.n_seg * G * D * 2
-        if sample_layers <= 0 and elapsed > budget_s:
-            break
+    try:
+        for li, st in enumerate(layers[:limit]):
+            k, v, cu = st.dense_host()
+            nk, nv, q = st.new_k.cpu(), st.new_v.cpu(), st.q.cpu()
+            cu_old = cu.tolist()
+            cu_new = [c + i for i, c in enumerate(cu_old)]
+            t0 = time.perf_counter()
+            k2 = torch_cpu.append_by_cat(k, nk, cu_old)
+            v2 = torch_cpu.append_by_cat(v, nv, cu_old)
+            torch_cpu.decode_attn(q, k2, v2, cu_new, scale)
+            elapsed += time.perf_counter() - t0
+            done += 1
+            bytes_done += cu_new[-1] * D * 2 * 2 + 2 * cfg.n_seg * G * D * 2
+            if sample_layers <= 0 and elapsed > budget_s:
+                break
+    finally:
+        torch.set_num_threads(prev)
     us = elapsed / done * 1e6
     return {"value": round(bytes_done / elapsed / 1e9, 4), "unit": "GB/s", "us_per_layer_step": round(us, 1),
-            "cores": 1, "kind": "port",
-            "sample": f"{done} of {cfg.layers} layers of one decode step ({cfg.name}), float64 C oracle"}
+            "cores": threads, "os_cpu_count": os.cpu_count(), "kind": "port",
+            "sample": f"{done} of {cfg.layers} layers of one decode step ({cfg.name}): torch.cat append + "
+                      f"per-segment float32 softmax attention (PyTorch, {threads} threads)"}
 
 
 if __name__ == "__main__":

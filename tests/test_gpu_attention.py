@@ -155,6 +155,52 @@ def test_out_of_order_layout_is_flagged(gpu):
     assert _lib.device_error() & _lib.DEVERR_ORDER
 
 
+@pytest.mark.parametrize("kernel", ["stream", "mfma", "valu"])
+@pytest.mark.parametrize("n_seg", [3, 80])
+def test_out_of_order_layout_leaves_workspace_valid(gpu, kernel, n_seg):
+    """An out-of-order layout whose segments cross workgroup boundaries is
+    flagged, and every workgroup then skips the split-K hand-off: the
+    arrival counters stay at zero, so a valid launch that follows on the same
+    workspace (same n_seg, so it is not cleared in between) is exact.
+    n_seg 3 takes the streaming kernel's direct prologue, 80 its table pass."""
+    G, D, n_wg = 4, 128, 4
+    rng = np.random.default_rng(5)
+    lens = [30] * n_seg
+    rows = 30 * n_seg + 10
+    # segment 0 placed last, the others shifted down: every segment but the
+    # moved one crosses a boundary of the four 1/4 ranges somewhere
+    base = np.array([30 * (n_seg - 1)] + [30 * (s - 1) for s in range(1, n_seg)], np.int64)
+    q = torch.zeros(n_seg, G, D, dtype=torch.bfloat16, device=gpu)
+    kv = torch.zeros(rows, D, dtype=torch.bfloat16, device=gpu)
+    cu = torch.from_numpy(cu_from_lens(lens)).to(gpu)
+    ws = fused_attn.AttnWorkspace(gpu)
+    print(f"out-of-order layout kernel={kernel} n_seg={n_seg}", flush=True)
+    fused_attn.decode_attn(q, kv, kv, cu, 0.1, seg_base=torch.from_numpy(base).to(gpu), kernel=kernel,
+                           n_wg=n_wg, workspace=ws)
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_ORDER
+    counters = ws.buf[:4 * n_seg].view(torch.int32)
+    assert int(counters.abs().sum().item()) == 0, "an arrival counter was left non-zero"
+    # a valid launch on the same workspace: in-order slack layout, ragged lengths
+    lens2 = [int(x) for x in rng.integers(1, 90, n_seg)]
+    base2 = np.zeros(n_seg, np.int64)
+    pos = 3
+    for s in range(n_seg):
+        base2[s] = pos
+        pos += lens2[s] + 2
+    qn = rand_rows(rng, n_seg * G, D, "bfloat16").reshape(n_seg, G, D)
+    kn, vn = rand_rows(rng, pos, D, "bfloat16"), rand_rows(rng, pos, D, "bfloat16")
+    cu2 = cu_from_lens(lens2)
+    ref = oracle.decode_attn(qn, kn, vn, cu2, D ** -0.5, base=base2, dtype=oracle.DT_BF16)
+    out = fused_attn.decode_attn(to_torch(qn, "bfloat16", gpu), to_torch(kn, "bfloat16", gpu),
+                                 to_torch(vn, "bfloat16", gpu), torch.from_numpy(cu2).to(gpu), D ** -0.5,
+                                 seg_base=torch.from_numpy(base2).to(gpu), kernel=kernel, n_wg=n_wg, workspace=ws)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
+    assert ok, msg
+
+
 def test_repeated_launches_reuse_workspace(gpu):
     """Counters are left at zero: many launches with different shapes stay correct."""
     for i, lens in enumerate([[300, 5000, 12], [7, 7, 7, 7, 7000], [1, 2, 3], [6000, 6000]]):

@@ -5,8 +5,10 @@ scores), then driven through ``decode_attention`` for several steps.  The
 simulation replays every step with the oracle: appends and compactions
 (bit-exact K/V, offsets), attention (2e-3 + 1e-2 |ref|), class-A scores
 (1e-6 + 1e-3 |ref|) and the planner's loaded segments.  The chunk top-k
-that the device computes from its own float32 scores is recorded and fed
-to the oracle planner, so both sides plan from the same chunks.
+that the device computes from its own float32 scores is checked against the
+oracle's ``topk_chunks(chunk_means(...))`` of the same recorded scores
+(exact unless the k-th and (k+1)-th chunk means are a float32 near-tie),
+and then fed to the oracle planner, so both sides plan from the same chunks.
 """
 import copy
 
@@ -51,6 +53,25 @@ def _recording(cls):
             self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
             return super()._plan(topk, off)
     return Rec
+
+
+def assert_topk_matches_oracle(got_per_sample, acc, offs, bounds_per_sample, k, what=""):
+    """The device's chosen chunks of every sample equal the oracle's top-k of
+    the chunk means of ``acc`` (float64 sums over each chunk's token bounds,
+    oracle/planner.py).  A different choice is accepted only where the
+    chunks involved are within float32 rounding of the k-th largest mean
+    (the device takes float32 prefix sums)."""
+    for b, got in enumerate(got_per_sample):
+        means = op.chunk_means(acc[offs[b]:offs[b + 1]], bounds_per_sample[b])
+        want = op.topk_chunks(means, k)
+        assert len(got) == len(want) and len(set(got)) == len(got), f"{what} sample {b}: {got} vs {want}"
+        assert all(0 <= c < len(means) for c in got), f"{what} sample {b}: {got}"
+        if sorted(got) == sorted(want):
+            continue
+        kth = sorted(means, reverse=True)[len(want) - 1]
+        tol = 1e-5 * max(abs(m) for m in means) + 1e-7
+        assert all(means[c] >= kth - tol for c in got), \
+            f"{what} sample {b}: device chose {sorted(got)}, oracle {sorted(want)} (means {means})"
 
 
 def _bits(t):
@@ -124,6 +145,8 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, monkeypatch)
         assert _lib.device_error() == 0, f"step {t}"
         # the plan made from the previous step's scores applies now
         if t > 0:
+            assert_topk_matches_oracle(cache.rec_topk[t - 1], cache.rec_acc[t - 1], offs,
+                                       cache._chunk_token_bounds, cache.config.top_k_chunks, f"step {t - 1}")
             o.seq_lens = [list(x) for x in lens]
             plan = o.step(cache.rec_topk[t - 1])
             n_plans += int(plan.any_change)

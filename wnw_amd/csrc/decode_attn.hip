@@ -80,6 +80,11 @@ struct SchedLds {
   int32_t P;       // effective number of workgroups (<= R)
   int32_t s_first, s_last;
   int32_t is_last;  // combine flag broadcast
+  // Set when the table is not in layout order (WNW_DEVERR_ORDER).  Every
+  // workgroup reads the whole table and comes to the same verdict, so all of
+  // them then skip the split-K hand-off: no arrival counter is touched and
+  // the workspace stays valid for the next launch.
+  int32_t order_bad;
   alignas(16) int32_t hdr[16][4];  // streaming kernel: merge slot headers (segment, length, base lo, base hi)
   int64_t ring_base[kRing];
   int32_t ring_len[kRing];
@@ -109,6 +114,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   if (tid == 0) {
     sl.s_first = 0x7fffffff;
     sl.s_last = -1;
+    sl.order_bad = 0;
   }
   const int64_t R = p.kv_rows;
   const int64_t P = effective_wgs(R);
@@ -170,10 +176,14 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       const int64_t b = p.base ? bs[u] : (int64_t)lo[u];
       if (len < 0) {  // corrupt offsets: treated as an empty segment
         raise_device_error(p.err, WNW_DEVERR_ORDER);
+        sl.order_bad = 1;
         len = 0;
       }
       // layout order: segment i must end before segment i + 1 starts
-      if (p.base && i + 1 < N && b + len > bn[u]) raise_device_error(p.err, WNW_DEVERR_ORDER);
+      if (p.base && i + 1 < N && b + len > bn[u]) {
+        raise_device_error(p.err, WNW_DEVERR_ORDER);
+        sl.order_bad = 1;
+      }
       (void)nxt;
       const bool owner = (i % (int)gridDim.x) == (int)pid;
       if (len == 0 || b < 0 || b + len > R) {
@@ -390,7 +400,7 @@ __device__ __forceinline__ void combine_segment(const AttnParams& p, int D, cons
 template <typename T, int NT>
 __device__ __forceinline__ void arrive_and_combine(const AttnParams& p, int D, SchedLds& sl, int64_t seg_base,
                                                    int64_t seg_len, int s) {
-  if (threadIdx.x == 0) sl.is_last = arrive(p, sl, seg_base, seg_len, s);
+  if (threadIdx.x == 0) sl.is_last = !sl.order_bad && arrive(p, sl, seg_base, seg_len, s);
   __syncthreads();
   if (!sl.is_last) return;  // workgroup-uniform
   combine_segment<T>(p, D, sl, seg_base, seg_len, s, threadIdx.x, NT);
@@ -1214,11 +1224,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     const int64_t nb = (int64_t)(((uint64_t)nhi << 32) | nlo);
     const int si = lane;
     int64_t len = si < p.n_seg ? llen : 0;
-    if (len < 0) {  // corrupt offsets: treated as an empty segment
-      raise_device_error(p.err, WNW_DEVERR_ORDER);
-      len = 0;
-    }
-    if (p.base && si + 1 < p.n_seg && lb + len > nb) raise_device_error(p.err, WNW_DEVERR_ORDER);
+    const bool neg = len < 0;
+    if (neg) len = 0;  // corrupt offsets: treated as an empty segment
+    const bool bad = neg || (p.base && si + 1 < p.n_seg && lb + len > nb);
+    if (bad) raise_device_error(p.err, WNW_DEVERR_ORDER);
+    const bool any_bad = __ballot(bad) != 0;
+    if (lane == 0) sl.order_bad = any_bad;
     if (si < p.n_seg && (len == 0 || lb < 0 || lb + len > R)) {
       if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
       if ((si % (int)gridDim.x) == (int)blockIdx.x) {
@@ -1400,7 +1411,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   // Both arrivals in one atomic instruction (lanes 0 and 1 of wave 0, one
   // memory round trip); each segment whose last partial this is merges.
   if (tid < 2) {
-    const int32_t ps = tid ? ps1 : ps0;
+    const int32_t ps = sl.order_bad ? -1 : (tid ? ps1 : ps0);
     bool f = false;
     if (ps >= 0)
       f = __hip_atomic_fetch_add(gptr_w<int32_t>(p.counters) + ps, 1, __ATOMIC_RELAXED,
@@ -1596,18 +1607,33 @@ __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
     p[i] = 0u;
 }
 
+// Raises a kernel's dynamic-LDS limit once per device (the attribute is a
+// property of the kernel on the device that is current when it is set).
+static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex& mu, const void* fn, int bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)done.size() <= dev) done.resize(dev + 1, 0);
+  if (!done[dev]) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return e;
+    done[dev] = 1;
+  }
+  return hipSuccess;
+}
+
 // Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
-// stream_lds_bytes (above 64 KB, so the limit is raised once per instance).
+// stream_lds_bytes (above 64 KB, so the limit is raised once per instance
+// and device).
 template <typename T, int D, int QD, bool XL>
 static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
   const int qslot = (ap.G * D * 2 + 255) & ~255;
   const int lds = stream_lds_bytes(D, kNW, qslot);
-  static std::once_flag once;
-  static hipError_t attr_err = hipSuccess;
-  std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)&attn_stream_kernel<T, D, kNW, QD, XL>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, stream_lds_bytes(D, kNW, 2048));
-  });
+  static std::mutex mu;
+  static std::vector<signed char> done;
+  const hipError_t attr_err = set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL>,
+                                                 stream_lds_bytes(D, kNW, 2048));
   if (attr_err != hipSuccess) return attr_err;
   hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap.q,
                      ap.k, ap.v, ap.cu, ap.base, ap.kv_rows, ap.n_seg, ap.G, ap);
