@@ -60,9 +60,10 @@ const char* wnw_last_error(void);
 int wnw_abi_version(void);
 
 /*
- * Prepares the current device (allocates the 256-byte device error word).
- * Call once per device before graph capture; other entry points call it
- * lazily otherwise.
+ * Prepares the current device: resolves the address of its device error
+ * word (a file-scope device array of the library, zero at load; nothing is
+ * allocated).  Call once per device before graph capture; other entry
+ * points call it lazily otherwise.
  */
 int wnw_init(void);
 
@@ -226,6 +227,32 @@ int wnw_decode_attn_ex(const void* q, const void* k, const void* v,
                        int dtype, void* out, void* workspace,
                        int64_t workspace_bytes, int kernel, int64_t n_wg,
                        void* stream);
+
+/* Limits of wnw_decode_attn_noalloc: the size of the library's own split-K
+ * scratch on each device, and the segments its counters region holds. */
+#define WNW_NOALLOC_SCRATCH_BYTES (16ll << 20)
+#define WNW_NOALLOC_MAX_SEG 4096
+
+/*
+ * wnw_decode_attn (AUTO kernel, grid from the device's occupancy) without a
+ * workspace argument: allocates nothing, ever.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split-K partials and arrival counters live in a
+ * file-scope device array of the library, WNW_NOALLOC_SCRATCH_BYTES per
+ * device, held until the process ends.  Limits: n_seg <= WNW_NOALLOC_MAX_SEG,
+ * and (grid + n_seg) partial slots of group * (head_dim + 2) floats must fit
+ * the array (n_seg 512, group 4, head_dim 128 needs ~1.6 MB); a larger call
+ * returns WNW_EINVAL with the bytes it would need.  Every call on a device
+ * shares that device's array, so calls that overlap on one device (other
+ * streams, other threads) race: order them on one stream.  The first call on
+ * a device clears the counters with a fill kernel on `stream`.
+ */
+int wnw_decode_attn_noalloc(const void* q, const void* k, const void* v,
+                            const int32_t* cu_k, const int64_t* seg_base,
+                            int64_t n_seg, int64_t group, int64_t head_dim,
+                            int64_t total_rows, int64_t kv_rows, float scale,
+                            int dtype, void* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Class-A token scores                                                      */

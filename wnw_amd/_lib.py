@@ -41,6 +41,8 @@ _SIGNATURES = {
                                _i64, _vp]),
     "wnw_decode_attn_ex": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp, _vp,
                                   _i64, _i32, _i64, _vp]),
+    "wnw_decode_attn_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
+                                       _vp]),
     "wnw_decode_attn_score_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "wnw_decode_attn_score": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
                                      _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp]),

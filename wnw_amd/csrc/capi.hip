@@ -28,9 +28,15 @@ int hip_fail(hipError_t e, const char* what) {
 static std::mutex g_mu;
 static std::vector<int32_t*> g_err_words;
 
-// Allocates (once per device, zero-filled synchronously) the word kernels
-// record WNW_DEVERR_* bits into.  Returns null if the allocation failed, in
-// which case kernels skip the recording but still refuse bad offsets.
+// The word kernels record WNW_DEVERR_* bits into: one per device, a
+// file-scope device array (zero at load, so nothing is allocated for it).
+// Host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns with that device current.
+static __device__ __align__(256) int32_t g_err_word[64];
+
+// The device address of the current device's error word (resolved once per
+// device), or null if the lookup failed, in which case kernels skip the
+// recording but still refuse bad offsets.
 int32_t* device_error_word() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
@@ -38,8 +44,7 @@ int32_t* device_error_word() {
   if ((int)g_err_words.size() <= dev) g_err_words.resize(dev + 1, nullptr);
   if (!g_err_words[dev]) {
     void* p = nullptr;
-    if (hipMalloc(&p, 256) != hipSuccess) return nullptr;
-    if (hipMemset(p, 0, 256) != hipSuccess) return nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_err_word)) != hipSuccess || !p) return nullptr;
     g_err_words[dev] = (int32_t*)p;
   }
   return g_err_words[dev];
@@ -65,8 +70,9 @@ extern "C" const char* wnw_last_error(void) { return wnw::g_err; }
 extern "C" int wnw_abi_version(void) { return 1; }
 
 extern "C" int wnw_init(void) {
-  if (!wnw::device_error_word()) {
-    wnw::set_error("could not allocate the device error word");
+  int32_t* w = wnw::device_error_word();
+  if (!w) {
+    wnw::set_error("could not resolve the device error word");
     return WNW_EHIP;
   }
   return WNW_OK;

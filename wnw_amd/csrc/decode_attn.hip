@@ -1590,17 +1590,43 @@ struct WsLayout {
   int64_t slots;
 };
 
-static WsLayout ws_layout(int64_t n_seg, int64_t G, int64_t D) {
-  const DeviceInfo& di = device_info();
+// Arrival counters for cap_seg segments first, then the (m, l) pairs and
+// the accumulators of `slots` partial slots.
+static WsLayout make_layout(int64_t cap_seg, int64_t slots, int64_t G, int64_t D) {
   WsLayout L;
-  L.slots = di.max_wg + n_seg;
+  L.slots = slots;
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   L.counters = 0;
-  L.ml = up(n_seg * 4);
+  L.ml = up(cap_seg * 4);
   L.acc = L.ml + up(L.slots * G * 2 * 4);
   L.total = L.acc + up(L.slots * G * D * 4);
   return L;
 }
+
+// Caller-owned workspace: sized before the grid is known, so for the
+// largest grid a launch may use.
+static WsLayout ws_layout(int64_t n_seg, int64_t G, int64_t D) {
+  return make_layout(n_seg, device_info().max_wg + n_seg, G, D);
+}
+
+// ---------------------------------------------------------------------------
+// The library's own attention scratch (wnw_decode_attn_noalloc)
+// ---------------------------------------------------------------------------
+// A file-scope device array: each device holds its own copy, at its own
+// address, for as long as the process lives.  Host code uses only the
+// per-device address from hipGetSymbolAddress (resolved once per device,
+// with that device current), never the array's name.  The counters region
+// is sized for WNW_NOALLOC_MAX_SEG segments whatever a call's n_seg, so
+// calls with different n_seg never turn partial bytes into counters; every
+// launch leaves the counters of its segments at zero, the others are never
+// touched, and the array is zero at load (cleared again on first use).
+static constexpr int64_t kNoAllocBytes = WNW_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t g_attn_scratch[kNoAllocBytes];
+
+struct ScratchSlot {
+  void* ptr = nullptr;
+  bool cleared = false;
+};
 
 __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -1696,15 +1722,43 @@ extern "C" int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void
 }
 
 namespace wnw {
+// The current device's scratch address (resolved once per device; the
+// counters region is cleared with a fill kernel on the first call, which
+// may be under graph capture, so no memset node is recorded).
+static int noalloc_scratch(hipStream_t st, void** out) {
+  static std::mutex mu;
+  static std::vector<ScratchSlot> slots;
+  int dev = 0;
+  WNW_CHECK_HIP(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)slots.size() <= dev) slots.resize(dev + 1);
+  ScratchSlot& sl = slots[dev];
+  if (!sl.ptr) {
+    void* p = nullptr;
+    WNW_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(g_attn_scratch)), "resolving the attention scratch");
+    WNW_CHECK_ARG(p != nullptr, "the attention scratch has no device address");
+    sl.ptr = p;
+  }
+  if (!sl.cleared) {
+    const int64_t n = (int64_t)WNW_NOALLOC_MAX_SEG;  // counters, 4 bytes each
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (uint32_t*)sl.ptr, n);
+    WNW_CHECK_HIP(hipGetLastError(), "clearing the attention scratch counters");
+    sl.cleared = true;
+  }
+  *out = sl.ptr;
+  return WNW_OK;
+}
+
 int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
                      const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     const AttnLogits* logits, int* logits_kept, void* stream) {
+                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc) {
   if (logits_kept) *logits_kept = 0;
   WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1ll << 30), "n_seg out of range: %lld", (long long)n_seg);
   if (n_seg == 0) return WNW_OK;
-  WNW_CHECK_ARG(q && cu_k && out && workspace && ((k && v) || kv_rows == 0), "null pointer argument");
+  WNW_CHECK_ARG(q && cu_k && out && (workspace || noalloc) && ((k && v) || kv_rows == 0),
+                "null pointer argument");
   WNW_CHECK_ARG(group >= 1 && group <= kMaxGroup, "group must be in [1, %d], got %lld", kMaxGroup,
                 (long long)group);
   WNW_CHECK_ARG(head_dim == 64 || head_dim == 128 || head_dim == 256,
@@ -1715,9 +1769,6 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   WNW_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
                     ((uintptr_t)out % 16) == 0,
                 "q, k, v and out must be 16-byte aligned");
-  const WsLayout L = ws_layout(n_seg, group, head_dim);
-  WNW_CHECK_ARG(workspace_bytes >= L.total, "workspace too small: %lld < %lld bytes",
-                (long long)workspace_bytes, (long long)L.total);
   int kern = kernel;
   if (kern == WNW_ATTN_AUTO)
     kern = (dtype != WNW_F32 && (head_dim == 64 || head_dim == 128))
@@ -1742,6 +1793,22 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
     P = std::min<int64_t>((int64_t)di.cus * (kern == WNW_ATTN_STREAM ? 1 : 2), by_rows);
   }
   P = std::max<int64_t>(1, std::min<int64_t>(P, di.max_wg));
+  WsLayout L;
+  if (noalloc) {
+    WNW_CHECK_ARG(n_seg <= WNW_NOALLOC_MAX_SEG, "the no-alloc entry point takes at most %d segments, got %lld",
+                  WNW_NOALLOC_MAX_SEG, (long long)n_seg);
+    L = make_layout(WNW_NOALLOC_MAX_SEG, P + n_seg, group, head_dim);
+    WNW_CHECK_ARG(L.total <= kNoAllocBytes,
+                  "this launch needs %lld bytes of split-K scratch; the no-alloc entry point holds %lld "
+                  "(fewer segments or a smaller group / head_dim fit)",
+                  (long long)L.total, (long long)kNoAllocBytes);
+    const int rc = noalloc_scratch((hipStream_t)stream, &workspace);
+    if (rc != WNW_OK) return rc;
+  } else {
+    L = ws_layout(n_seg, group, head_dim);
+    WNW_CHECK_ARG(workspace_bytes >= L.total, "workspace too small: %lld < %lld bytes",
+                  (long long)workspace_bytes, (long long)L.total);
+  }
 
   AttnParams ap;
   ap.q = q;
@@ -1795,7 +1862,7 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
                                   int kernel, int64_t n_wg, void* stream) {
   return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
                           dtype, out, workspace, workspace_bytes, kernel, n_wg, nullptr, nullptr, nullptr,
-                          stream);
+                          stream, false);
 }
 
 extern "C" int wnw_decode_attn(const void* q, const void* k, const void* v, const int32_t* cu_k,
@@ -1805,4 +1872,12 @@ extern "C" int wnw_decode_attn(const void* q, const void* k, const void* v, cons
                                void* stream) {
   return wnw_decode_attn_ex(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows,
                             scale, dtype, out, workspace, workspace_bytes, WNW_ATTN_AUTO, 0, stream);
+}
+
+extern "C" int wnw_decode_attn_noalloc(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                                       const int64_t* seg_base, int64_t n_seg, int64_t group,
+                                       int64_t head_dim, int64_t total_rows, int64_t kv_rows, float scale,
+                                       int dtype, void* out, void* stream) {
+  return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
+                          dtype, out, nullptr, 0, WNW_ATTN_AUTO, 0, nullptr, nullptr, nullptr, stream, true);
 }

@@ -459,7 +459,7 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   int kept = 0;
   int rc = decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
                             dtype, out, workspace, attn_ws, WNW_ATTN_AUTO, 0, lse, room ? &lg : nullptr, &kept,
-                            stream);
+                            stream, false);
   if (rc != WNW_OK || n_seg == 0 || max_audio == 0) return rc;
   if (kept) {
     LogitScoreParams lp;

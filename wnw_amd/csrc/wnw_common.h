@@ -39,7 +39,7 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                      const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     const AttnLogits* logits, int* logits_kept, void* stream);
+                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc);
 
 #define WNW_CHECK_ARG(cond, ...)       \
   do {                                 \
