@@ -97,6 +97,7 @@ class LayerState:
         base[1:] = np.cumsum(cap)[:-1]
         self.pool_rows = int(cap.sum())
         self.lens0 = lens
+        self.rows_est = int(lens.sum())  # sizes the grid; the kernel reads the exact rows from cu
         self.base = torch.from_numpy(base).to(device)
         self.cap = torch.from_numpy(cap.astype(np.int32)).to(device)
         cu = np.zeros(self.n + 1, np.int32)
@@ -170,7 +171,7 @@ def main():
         for st in layers:
             cu_old, cu_new = st.cu[parity], st.cu[1 - parity]
             append_inplace(st.k, st.v, st.new_k, st.new_v, cu_old, cu_new, st.base, st.cap)
-            fused_attn.decode_attn(st.q, st.k, st.v, cu_new, scale, seg_base=st.base, total_rows=st.pool_rows,
+            fused_attn.decode_attn(st.q, st.k, st.v, cu_new, scale, seg_base=st.base, total_rows=st.rows_est,
                                    out=st.out, workspace=ws, kernel=args.kernel)
 
     def append_launches(parity: int):
@@ -179,7 +180,7 @@ def main():
 
     def attn_launches():
         for st in layers:
-            fused_attn.decode_attn(st.q, st.k, st.v, st.cu[0], scale, seg_base=st.base, total_rows=st.pool_rows,
+            fused_attn.decode_attn(st.q, st.k, st.v, st.cu[0], scale, seg_base=st.base, total_rows=st.rows_est,
                                    out=st.out, workspace=ws, kernel=args.kernel)
 
     stream = torch.cuda.Stream(device=dev)

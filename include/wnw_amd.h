@@ -13,8 +13,9 @@
  * the rows of (sequence b, KV head h); cu_seqlens is int32 [n_seg + 1] with
  * cu[0] = 0 and segment s = logical rows [cu[s], cu[s+1]).  An optional int64
  * seg_base[n_seg] gives the physical row of each segment's first row, so a
- * cache may keep per-segment slack and append in place; when seg_base is
- * NULL the physical row of logical row j is j (the reference's dense layout).
+ * cache may keep per-segment slack, append in place and place segments in
+ * any order; when seg_base is NULL the physical row of logical row j is j
+ * (the reference's dense layout).
  *
  * Device-side bounds: kernels that follow offsets read from device memory
  * check every derived row against the row counts passed here and, instead
@@ -42,8 +43,7 @@ extern "C" {
 
 /* device error bits recorded by kernels (wnw_device_error) */
 #define WNW_DEVERR_BOUNDS 1   /* an offset pointed outside the given rows  */
-#define WNW_DEVERR_ORDER 2    /* cu_seqlens decreasing, or segments not in
-                                 index order in the physical rows         */
+#define WNW_DEVERR_ORDER 2    /* cu_seqlens decreasing                     */
 #define WNW_DEVERR_CAPACITY 4 /* in-place append beyond segment capacity   */
 
 /* attention kernel selection (wnw_decode_attn_ex) */
@@ -199,14 +199,16 @@ int wnw_workspace_init(void* workspace, int64_t workspace_bytes, void* stream);
  * where q is [n_seg, group, head_dim] (q head h = kv * group + g,
  * session.py:81-83) and K_s/V_s are the rows of segment s.  fp32 softmax
  * and accumulation; out has the dtype of q/K/V.  An empty segment yields
- * zeros.  kv_rows is the number of rows allocated in k and v: the kernel
- * splits this physical row range evenly over its workgroups, so the cost
- * does not depend on how ragged the segments are.  Segments must be laid
- * out in index order (seg_base[s] + len[s] <= seg_base[s+1]; the dense
- * layout, seg_base NULL, always is); a violation sets WNW_DEVERR_ORDER and
- * a segment outside [0, kv_rows) sets WNW_DEVERR_BOUNDS and yields NaN.
- * total_rows (an upper bound of cu_k[n_seg]) is checked for sign only and
- * kept for signature stability.  q, k, v and out must be 16-byte aligned.
+ * zeros (as the reference's default varlen_attn path does for an empty
+ * key range; no decode-time segment is ever empty, since each holds the
+ * step's own row).  The kernel splits the logical rows [0, cu_k[n_seg])
+ * evenly over its workgroups (it reads cu_k[n_seg] itself, so a launch
+ * captured in a graph stays right as segments grow), so the cost does not
+ * depend on how ragged the segments are.  total_rows, an estimate of
+ * cu_k[n_seg], only sizes the grid.  kv_rows is the number of rows allocated
+ * in k and v: a segment outside [0, kv_rows) sets WNW_DEVERR_BOUNDS and
+ * yields NaN.  Segments may sit anywhere in k / v, in any order; decreasing
+ * offsets set WNW_DEVERR_ORDER.  q, k, v and out must be 16-byte aligned.
  */
 int wnw_decode_attn(const void* q, const void* k, const void* v,
                     const int32_t* cu_k, const int64_t* seg_base,
@@ -214,6 +216,33 @@ int wnw_decode_attn(const void* q, const void* k, const void* v,
                     int64_t total_rows, int64_t kv_rows, float scale,
                     int dtype, void* out, void* workspace,
                     int64_t workspace_bytes, void* stream);
+
+/*
+ * The step's append and the decode attention in one launch, for a cache
+ * with per-segment slack.  Replaces decode_before_attn's two full-layer
+ * interleave_append copies (src/algorithms/wnw/code/cache.py:497-515,
+ * src/common/kv/kernels.py:45-73) plus the q1_decode_attn / varlen_attn
+ * call (src/common/kv/fused_attn.py:47-65, src/algorithms/wnw/code/
+ * session.py:90-106).  For every segment s, with len = cu_old[s+1] -
+ * cu_old[s]: new_k/new_v[s] becomes row seg_base[s] + len of k_pool/v_pool,
+ * cu_new = cu_old + arange(n_seg + 1) (the reference's cache.py:504), and
+ * out is wnw_decode_attn over the len + 1 rows of every segment.  The
+ * streaming kernel reads the new rows from new_k/new_v and writes them into
+ * the pools itself (one launch); other kernels (fp32, head_dim 256, group
+ * > 8) run wnw_append_inplace first.  total_rows (an estimate of
+ * cu_old[n_seg] + n_seg) sizes the grid.
+ * seg_cap[s] bounds len + 1 (WNW_DEVERR_CAPACITY otherwise; the row is then
+ * attended but not stored).  cu_new must not alias cu_old.  new_k/new_v
+ * 16-byte aligned.
+ */
+int wnw_decode_attn_append(const void* q, void* k_pool, void* v_pool,
+                           const void* new_k, const void* new_v,
+                           const int32_t* cu_old, int32_t* cu_new,
+                           const int64_t* seg_base, const int32_t* seg_cap,
+                           int64_t n_seg, int64_t group, int64_t head_dim,
+                           int64_t total_rows, int64_t pool_rows, float scale,
+                           int dtype, void* out, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /*
  * wnw_decode_attn with an explicit kernel choice (WNW_ATTN_*) and an
@@ -297,6 +326,24 @@ int wnw_decode_attn_score(const void* q, const void* k, const void* v,
                           const int32_t* score_offsets, int64_t acc_len,
                           int64_t max_audio, void* workspace,
                           int64_t workspace_bytes, void* stream);
+
+/*
+ * wnw_decode_attn_append followed by the class-A scoring of
+ * wnw_decode_attn_score over the post-append segments (cu_new): the step's
+ * append + q1_decode_attn_score (src/common/kv/fused_attn.py:124-156) of a
+ * foldable layer (src/algorithms/wnw/code/cache.py:546-566).  Same
+ * workspace as wnw_decode_attn_score.
+ */
+int wnw_decode_attn_score_append(
+    const void* q, void* k_pool, void* v_pool, const void* new_k,
+    const void* new_v, const int32_t* cu_old, int32_t* cu_new,
+    const int64_t* seg_base, const int32_t* seg_cap, int64_t n_seg,
+    int64_t group, int64_t head_dim, int64_t total_rows, int64_t pool_rows,
+    float scale, int dtype, void* out, const int32_t* ca_kv_mask,
+    int64_t num_kv_heads, const int32_t* audio_starts,
+    const int32_t* audio_ends, float* score_acc, const int32_t* score_offsets,
+    int64_t acc_len, int64_t max_audio, void* workspace,
+    int64_t workspace_bytes, void* stream);
 
 /* Workspace of wnw_fused_score_accumulate (partial softmax statistics). */
 int64_t wnw_fused_score_workspace_bytes(int64_t n_samples, int64_t n_heads);

@@ -143,45 +143,56 @@ def test_slack_layout_many_workgroups(gpu):
         assert ok, msg
 
 
-def test_out_of_order_layout_is_flagged(gpu):
-    """Segments must be laid out in index order; a violation sets the device error word."""
-    n, G, D = 3, 4, 128
-    q = torch.zeros(n, G, D, dtype=torch.bfloat16, device=gpu)
-    k = torch.zeros(100, D, dtype=torch.bfloat16, device=gpu)
-    cu = torch.tensor([0, 10, 20, 30], dtype=torch.int32, device=gpu)
-    base = torch.tensor([50, 0, 70], dtype=torch.int64, device=gpu)  # segment 0 after segment 1
-    fused_attn.decode_attn(q, k, k, cu, 0.1, seg_base=base)
-    torch.cuda.synchronize()
-    assert _lib.device_error() & _lib.DEVERR_ORDER
+@pytest.mark.parametrize("kernel", ["stream", "mfma", "valu"])
+@pytest.mark.parametrize("n_seg", [5, 90])
+def test_segments_in_any_physical_order(gpu, kernel, n_seg):
+    """The work split runs over logical rows, so segments may sit anywhere in
+    the K/V arrays, in any order and with gaps (n_seg 5: the streaming
+    kernel's direct prologue; 90: its table pass)."""
+    rng = np.random.default_rng(n_seg)
+    lens = [int(x) for x in rng.integers(0, 700, n_seg)]
+    order = rng.permutation(n_seg)
+    base = np.zeros(n_seg, np.int64)
+    pos = 7
+    for s in order:
+        base[s] = pos
+        pos += lens[s] + int(rng.integers(0, 5))
+    for n_wg in (0, 13):
+        got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", kernel=kernel, seed=n_seg + n_wg, base=base,
+                             pool_rows=pos + 2, n_wg=n_wg)
+        ok, msg = allclose_report(got, ref, ATOL, RTOL)
+        assert ok, msg
 
 
 @pytest.mark.parametrize("kernel", ["stream", "mfma", "valu"])
 @pytest.mark.parametrize("n_seg", [3, 80])
-def test_out_of_order_layout_leaves_workspace_valid(gpu, kernel, n_seg):
-    """An out-of-order layout whose segments cross workgroup boundaries is
-    flagged, and every workgroup then skips the split-K hand-off: the
-    arrival counters stay at zero, so a valid launch that follows on the same
-    workspace (same n_seg, so it is not cleared in between) is exact.
-    n_seg 3 takes the streaming kernel's direct prologue, 80 its table pass."""
+def test_decreasing_offsets_leave_workspace_valid(gpu, kernel, n_seg):
+    """Decreasing offsets (a corrupt table: segments overlap in the logical
+    row space) are flagged, and every workgroup then skips the split-K
+    hand-off: the arrival counters stay at zero, so a valid launch that
+    follows on the same workspace (same n_seg, so it is not cleared in
+    between) is exact.  n_seg 3 takes the streaming kernel's direct
+    prologue, 80 its table pass; every segment crosses a boundary of the
+    four workgroup ranges."""
     G, D, n_wg = 4, 128, 4
     rng = np.random.default_rng(5)
-    lens = [30] * n_seg
-    rows = 30 * n_seg + 10
-    # segment 0 placed last, the others shifted down: every segment but the
-    # moved one crosses a boundary of the four 1/4 ranges somewhere
-    base = np.array([30 * (n_seg - 1)] + [30 * (s - 1) for s in range(1, n_seg)], np.int64)
+    cu_bad = np.array([30 * s for s in range(n_seg + 1)], np.int32)
+    # segment 0 = rows [0, 45); segment 1's offsets decrease (45 -> 40);
+    # segment 2 = [40, 90) overlaps segment 0 in the logical row space
+    cu_bad[1] = 45
+    cu_bad[2] = 40
+    rows = int(cu_bad[-1]) + 10
     q = torch.zeros(n_seg, G, D, dtype=torch.bfloat16, device=gpu)
     kv = torch.zeros(rows, D, dtype=torch.bfloat16, device=gpu)
-    cu = torch.from_numpy(cu_from_lens(lens)).to(gpu)
     ws = fused_attn.AttnWorkspace(gpu)
-    print(f"out-of-order layout kernel={kernel} n_seg={n_seg}", flush=True)
-    fused_attn.decode_attn(q, kv, kv, cu, 0.1, seg_base=torch.from_numpy(base).to(gpu), kernel=kernel,
-                           n_wg=n_wg, workspace=ws)
+    print(f"decreasing offsets kernel={kernel} n_seg={n_seg}", flush=True)
+    fused_attn.decode_attn(q, kv, kv, torch.from_numpy(cu_bad).to(gpu), 0.1, kernel=kernel, n_wg=n_wg,
+                           workspace=ws)
     torch.cuda.synchronize()
     assert _lib.device_error() & _lib.DEVERR_ORDER
     counters = ws.buf[:4 * n_seg].view(torch.int32)
     assert int(counters.abs().sum().item()) == 0, "an arrival counter was left non-zero"
-    # a valid launch on the same workspace: in-order slack layout, ragged lengths
+    # a valid launch on the same workspace: slack layout, ragged lengths
     lens2 = [int(x) for x in rng.integers(1, 90, n_seg)]
     base2 = np.zeros(n_seg, np.int64)
     pos = 3
@@ -194,63 +205,10 @@ def test_out_of_order_layout_leaves_workspace_valid(gpu, kernel, n_seg):
     ref = oracle.decode_attn(qn, kn, vn, cu2, D ** -0.5, base=base2, dtype=oracle.DT_BF16)
     out = fused_attn.decode_attn(to_torch(qn, "bfloat16", gpu), to_torch(kn, "bfloat16", gpu),
                                  to_torch(vn, "bfloat16", gpu), torch.from_numpy(cu2).to(gpu), D ** -0.5,
-                                 seg_base=torch.from_numpy(base2).to(gpu), kernel=kernel, n_wg=n_wg, workspace=ws)
+                                 seg_base=torch.from_numpy(base2).to(gpu), total_rows=int(cu2[-1]), kernel=kernel,
+                                 n_wg=n_wg, workspace=ws)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
-    ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
-    assert ok, msg
-
-
-def test_repeated_launches_reuse_workspace(gpu):
-    """Counters are left at zero: many launches with different shapes stay correct."""
-    for i, lens in enumerate([[300, 5000, 12], [7, 7, 7, 7, 7000], [1, 2, 3], [6000, 6000]]):
-        got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", seed=20 + i)
-        ok, msg = allclose_report(got, ref, ATOL, RTOL)
-        assert ok, msg
-
-
-def test_cfg1_fp32_and_bf16(gpu):
-    """Config 1 (fp32 plumbing) through the VALU kernel, and its bf16 cast through MFMA."""
-    cfg = workloads.config1()
-    lens = cfg.lengths[0] + 1
-    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "float32", seed=0)
-    ok, msg = allclose_report(got, ref, 1e-4, 1e-3)
-    assert ok, msg
-    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=0)
-    ok, msg = allclose_report(got, ref, ATOL, RTOL)
-    assert ok, msg
-
-
-@pytest.mark.parametrize("name,layer", [("cfg2", 0), ("cfg3", 0), ("cfg5", 0)])
-def test_config_layer_full_size(gpu, name, layer):
-    """One full-size layer of configs 2, 3 and 5 against the float64 oracle."""
-    cfg = workloads.CONFIGS[name]()
-    lens = cfg.lengths[layer] + 1
-    kvs = float(cfg.kv_scale[layer].mean())
-    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=layer, kv_scale=kvs)
-    ok, msg = allclose_report(got, ref, ATOL, RTOL)
-    print(name, msg)
-    assert ok, msg
-
-
-def test_large_scores_are_stable(gpu):
-    """Keys scaled x8: scores up to ~+-100 must not overflow the online softmax."""
-    got, ref = _run_case(gpu, [2000, 33, 517], 4, 128, "bfloat16", seed=30, kv_scale=8.0)
-    ok, msg = allclose_report(got, ref, ATOL, RTOL)
-    assert ok, msg
-
-
-def test_q1_decode_attn_reference_signature(gpu):
-    rng = np.random.default_rng(31)
-    lens = [100, 3000, 7]
-    cu = cu_from_lens(lens)
-    q = rand_rows(rng, 3 * 4, 128, "bfloat16").reshape(3, 4, 128)
-    k = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
-    v = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
-    ref = oracle.decode_attn(q, k, v, cu, 0.1, dtype=oracle.DT_BF16)
-    out = fused_attn.q1_decode_attn(to_torch(q, "bfloat16", gpu), to_torch(k, "bfloat16", gpu),
-                                    to_torch(v, "bfloat16", gpu), torch.from_numpy(cu).to(gpu), 0.1)
-    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (3, 4, 128)
     ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
     assert ok, msg
 
@@ -396,3 +354,151 @@ def test_random_configurations(gpu, seed):
     atol, rtol = _tol(c["dtype"])
     ok, msg = allclose_report(got, ref, atol, rtol)
     assert ok, f"{c['kernel']} {c['dtype']} D={c['D']} G={c['G']} n_seg={len(c['lens'])} n_wg={c['n_wg']}: {msg}"
+
+
+# ---------------------------------------------------------------------------
+# fused append (wnw_decode_attn_append): the step's row of every segment is
+# written into its slack, and attention covers it
+# ---------------------------------------------------------------------------
+def _append_case(dev, lens, G, D, dtype, seed, shuffle=True, short_cap=None, score=None):
+    """Random slack layout (segments in a shuffled physical order with gaps),
+    one fused append + attention; returns what to compare."""
+    rng = np.random.default_rng(seed)
+    n = len(lens)
+    lens = np.asarray(lens, np.int64)
+    cap = lens + 1 + rng.integers(0, 6, n)
+    if short_cap is not None:
+        cap[short_cap] = lens[short_cap]  # no room for the new row
+    order = rng.permutation(n) if shuffle else np.arange(n)
+    base = np.zeros(n, np.int64)
+    pos = int(rng.integers(0, 9))
+    for s in order:
+        base[s] = pos
+        # a segment without room gets a gap row after it, so the reference's
+        # copy of its (unstored) new row never lands in a neighbour
+        pos += int(cap[s]) + int(rng.integers(0, 3)) + (1 if s == short_cap else 0)
+    pool = pos + 4
+    k = rand_rows(rng, pool, D, dtype)
+    v = rand_rows(rng, pool, D, dtype)
+    nk, nv = rand_rows(rng, n, D, dtype), rand_rows(rng, n, D, dtype)
+    q = rand_rows(rng, n * G, D, dtype).reshape(n, G, D)
+    cu_old = cu_from_lens(lens)
+    cu_new = cu_old + np.arange(n + 1, dtype=np.int32)
+    want_k, want_v = k.copy(), v.copy()
+    ok_rows = [s for s in range(n) if lens[s] + 1 <= cap[s]]
+    want_k[base[ok_rows] + lens[ok_rows]] = nk[ok_rows]
+    want_v[base[ok_rows] + lens[ok_rows]] = nv[ok_rows]
+    # the attention sees every new row (read from new_k / new_v)
+    att_k, att_v = k.copy(), v.copy()
+    att_k[base + lens] = nk
+    att_v[base + lens] = nv
+    code = DTYPE_CODES[dtype]
+    scale = D ** -0.5
+    ref = oracle.decode_attn(q, att_k, att_v, cu_new, scale, base=base, dtype=code)
+    tk, tv = to_torch(k, dtype, dev), to_torch(v, dtype, dev)
+    t32 = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(dev)  # noqa: E731
+    tcu_new = torch.full((n + 1,), -7, dtype=torch.int32, device=dev)
+    print(f"append case n_seg={n} G={G} D={D} {dtype} seed={seed} short_cap={short_cap}", flush=True)
+    app = (to_torch(nk, dtype, dev), to_torch(nv, dtype, dev), tcu_new, t32(cap))
+    tb = torch.from_numpy(base).to(dev)
+    if score is None:
+        out = fused_attn.decode_attn(to_torch(q, dtype, dev), tk, tv, t32(cu_old), scale, seg_base=tb,
+                                     total_rows=int(cu_new[-1]), append=app)
+        extra = None
+    else:
+        H, mask, a_s, a_e = score
+        offs = np.concatenate([[0], np.cumsum(np.array(a_e) - np.array(a_s))]).astype(np.int32)
+        acc0 = rng.random(int(offs[-1])).astype(np.float32)
+        ref_acc = oracle.attn_scores(q, att_k, cu_new, scale, mask, H, a_s, a_e, offs, acc0.astype(np.float64),
+                                     base=base, dtype=code)
+        acc = torch.from_numpy(acc0).to(dev)
+        out = fused_attn.q1_decode_attn_score(
+            to_torch(q, dtype, dev), tk, tv, t32(cu_old), scale, t32(mask), H, t32(a_s), t32(a_e), acc, t32(offs),
+            seg_base=tb, total_rows=int(cu_new[-1]), max_audio=int(max(np.array(a_e) - np.array(a_s))),
+            append=app)
+        extra = (acc, ref_acc)
+    torch.cuda.synchronize()
+    err = _lib.device_error()
+    got = oracle.to_f64(from_torch(out, dtype), code)
+    return dict(got=got, ref=ref, err=err, k=from_torch(tk, dtype), v=from_torch(tv, dtype), want_k=want_k,
+                want_v=want_v, cu_new=tcu_new.cpu().numpy(), want_cu=cu_new, extra=extra)
+
+
+def _check_append(r, dtype, err=0):
+    assert r["err"] == err
+    np.testing.assert_array_equal(r["cu_new"], r["want_cu"])
+    np.testing.assert_array_equal(r["k"], r["want_k"], err_msg="K pool after the append")
+    np.testing.assert_array_equal(r["v"], r["want_v"], err_msg="V pool after the append")
+    ok, msg = allclose_report(r["got"], r["ref"], *_tol(dtype))
+    assert ok, msg
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("G,D", [(1, 128), (4, 128), (7, 128), (8, 128), (4, 64), (8, 64)])
+def test_fused_append_direct(gpu, dtype, G, D):
+    """Up to 64 segments (the direct prologue), empty-before-append and
+    one-row segments included, segments in a shuffled physical order."""
+    lens = [0, 1, 15, 16, 17, 31, 7565, 513, 1000, 2, 300, 0, 64, 65]
+    _check_append(_append_case(gpu, lens, G, D, dtype, seed=G * 10 + D), dtype)
+
+
+@pytest.mark.parametrize("n_seg", [65, 300, 1100])
+def test_fused_append_table_pass(gpu, n_seg):
+    """More than 64 segments: the workgroup table pass (with its LDS ring, or
+    the direct table reads beyond it)."""
+    rng = np.random.default_rng(n_seg)
+    lens = [int(x) for x in rng.integers(0, 900 if n_seg < 1000 else 90, n_seg)]
+    _check_append(_append_case(gpu, lens, 4, 128, "bfloat16", seed=n_seg), "bfloat16")
+
+
+@pytest.mark.parametrize("dtype,G,D", [("float32", 4, 128), ("bfloat16", 16, 128), ("bfloat16", 4, 256)])
+def test_fused_append_other_kernels(gpu, dtype, G, D):
+    """Where the streaming kernel does not apply (fp32, group > 8, head_dim
+    256) the entry point runs the in-place append, then the attention."""
+    lens = [0, 3, 700, 129, 1, 2000, 45]
+    _check_append(_append_case(gpu, lens, G, D, dtype, seed=3), dtype)
+
+
+def test_fused_append_capacity_is_refused(gpu):
+    """A segment without room for its new row: WNW_DEVERR_CAPACITY, and the
+    row is not stored (the neighbouring rows keep their bytes)."""
+    lens = [40, 300, 5, 77]
+    r = _append_case(gpu, lens, 4, 128, "bfloat16", seed=9, short_cap=1)
+    _check_append(r, "bfloat16", err=_lib.DEVERR_CAPACITY)
+
+
+@pytest.mark.parametrize("keep_logits", [True])
+def test_fused_append_with_scores(gpu, keep_logits):
+    """Append + attention + class-A scores of the appended segments."""
+    H = 4
+    lens = [40, 300, 17, 1000, 64, 2, 513, 90]  # B = 2
+    r = _append_case(gpu, lens, 4, 128, "bfloat16", seed=4, score=(H, [0, 1, 0, 1], [3, 0], [17, 2]))
+    _check_append(r, "bfloat16")
+    acc, ref_acc = r["extra"]
+    ok, msg = allclose_report(acc.cpu().numpy().astype(np.float64), ref_acc, 1e-6, 1e-3)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("n_seg", [6, 100])
+def test_total_rows_only_sizes_the_grid(gpu, n_seg):
+    """The kernel reads cu[-1] itself: a stale total_rows (as a captured
+    graph keeps while the segments grow) changes the grid size at most,
+    never the result."""
+    rng = np.random.default_rng(31 + n_seg)
+    lens = [int(x) for x in rng.integers(1, 2000, n_seg)]
+    G, D = 4, 128
+    cu = cu_from_lens(lens)
+    T = int(cu[-1])
+    q = rand_rows(rng, n_seg * G, D, "bfloat16").reshape(n_seg, G, D)
+    k, v = rand_rows(rng, T, D, "bfloat16"), rand_rows(rng, T, D, "bfloat16")
+    ref = oracle.decode_attn(q, k, v, cu, D ** -0.5, dtype=oracle.DT_BF16)
+    base = torch.from_numpy(cu[:-1].astype(np.int64)).to(gpu)
+    for total in (T // 3, T, 5 * T):
+        print(f"total_rows={total} actual={T} n_seg={n_seg}", flush=True)
+        out = fused_attn.decode_attn(to_torch(q, "bfloat16", gpu), to_torch(k, "bfloat16", gpu),
+                                     to_torch(v, "bfloat16", gpu), torch.from_numpy(cu).to(gpu), D ** -0.5,
+                                     seg_base=base, total_rows=total)
+        torch.cuda.synchronize()
+        assert _lib.device_error() == 0
+        ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
+        assert ok, f"total_rows={total}: {msg}"

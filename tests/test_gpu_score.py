@@ -43,7 +43,8 @@ def _attn_score_case(dev, lens, H, G, D, mask, a_s, a_e, seed, base=None, pool_r
     out = fused_attn.q1_decode_attn_score(
         to_torch(q, dtype, dev), to_torch(k, dtype, dev), to_torch(v, dtype, dev), t(cu), scale,
         t(mask), H, t(a_s), t(a_e), acc, t(offs),
-        seg_base=None if base is None else t(base, torch.int64), max_audio=int(max(np.array(a_e) - np.array(a_s))),
+        seg_base=None if base is None else t(base, torch.int64), total_rows=int(cu[-1]),
+        max_audio=int(max(np.array(a_e) - np.array(a_s))),
         keep_logits=keep_logits)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0

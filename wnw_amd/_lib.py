@@ -17,6 +17,7 @@ WNW_OK, WNW_EINVAL, WNW_EHIP, WNW_ENOTSUP = 0, 1, 2, 3
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ATTN_AUTO, ATTN_MFMA, ATTN_VALU, ATTN_STREAM = 0, 1, 2, 3
 DEVERR_BOUNDS, DEVERR_ORDER, DEVERR_CAPACITY = 1, 2, 4
+NOALLOC_SCRATCH_BYTES, NOALLOC_MAX_SEG = 16 << 20, 4096
 
 _TORCH_DTYPES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 
@@ -41,6 +42,9 @@ _SIGNATURES = {
                                _i64, _vp]),
     "wnw_decode_attn_ex": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp, _vp,
                                   _i64, _i32, _i64, _vp]),
+    "wnw_decode_attn_append": (_i32, [_vp] * 9 + [_i64] * 5 + [_f32, _i32, _vp, _vp, _i64, _vp]),
+    "wnw_decode_attn_score_append": (_i32, [_vp] * 9 + [_i64] * 5 + [_f32, _i32, _vp, _vp, _i64, _vp, _vp, _vp,
+                                                                 _vp, _i64, _i64, _vp, _i64, _vp]),
     "wnw_decode_attn_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp,
                                        _vp]),
     "wnw_decode_attn_score_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),

@@ -6,19 +6,25 @@
 //     out[s, g] = sum_r softmax_r(scale * q[s, g] . K[r]) * V[r]
 // over the rows r of segment s.
 //
-// Work split ("stream-K" over the physical row space).  The kv_rows physical
-// rows of K/V are cut into P equal contiguous ranges, one per workgroup, so
-// every workgroup streams the same number of bytes however ragged the
-// segment lengths are.  Segments
-// must be laid out in index order (base[s] + len[s] <= base[s+1]; the dense
-// layout and a per-segment slack layout both are); the kernel checks it.
-// A range may cover the tail of one segment, whole segments and the head of
-// another; each (workgroup, segment) overlap is a "piece".  A piece that is a
-// whole segment writes the output directly.  The others write an (m, l, acc)
-// partial to slot (p + s) -- unique because ranges and segments are both
-// monotone in the row space -- and bump the segment's arrival counter; the
-// last arriver merges the partials by log-sum-exp and writes the output (no
-// second kernel launch).
+// Work split ("stream-K" over the logical row space).  The logical rows
+// [0, cu[n_seg]) -- segment s owns [cu[s], cu[s+1]) -- are cut into P equal
+// contiguous ranges, one per workgroup, so every workgroup streams the same
+// number of bytes however ragged the segment lengths are.  Logical row j of
+// segment s lives at physical row base[s] + (j - cu[s]) (base = cu without
+// seg_base), so segments may sit anywhere in the K/V arrays, in any order,
+// with any slack between them.  A range may cover the tail of one segment,
+// whole segments and the head of another; each (workgroup, segment) overlap
+// is a "piece".  A piece that is a whole segment writes the output directly.
+// The others write an (m, l, acc) partial to slot (p + s) -- unique because
+// ranges and segments are both monotone in the logical row space -- and bump
+// the segment's arrival counter; the last arriver merges the partials by
+// log-sum-exp and writes the output (no second kernel launch).
+//
+// Fused append (streaming kernel, APPEND): every segment first gains the
+// step's new row, new_k/new_v[s], at physical row base[s] + len_old[s]
+// (len_old from cu); the step that covers that row reads it from new_k/new_v
+// instead of the pool, and the wave that processed it writes it into the
+// pool from LDS.  cu_out = cu + arange(n_seg + 1) is written by workgroup 0.
 //
 // Three kernels implement this split.  The streaming kernel (bf16/f16, D 64 or
 // 128, G <= 8; the default there) gives each wave a quarter of its
@@ -47,9 +53,9 @@ static constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
   const void* q;        // [n_seg, G, D]
-  const void* k;        // [kv_rows, D]
-  const void* v;        // [kv_rows, D]
-  const int32_t* cu;    // [n_seg + 1] logical offsets
+  const void* k;        // [phys_rows, D]
+  const void* v;        // [phys_rows, D]
+  const int32_t* cu;    // [n_seg + 1] logical offsets (before the append, with APPEND)
   const int64_t* base;  // [n_seg] physical first row, or null (= cu)
   void* out;            // [n_seg, G, D]
   float* part_acc;      // [slots, G, D]
@@ -57,7 +63,8 @@ struct AttnParams {
   int32_t* counters;    // [n_seg]
   float* lse;           // [n_seg, G, 2] final (max, sum) of each softmax, log2 domain, or null
   int32_t* err;
-  int64_t kv_rows;
+  uint64_t split_inv;  // ceil(2^64 / (gridDim.x * kSplitWaves)): range bounds without a division
+  int64_t phys_rows;   // rows of k / v (bounds)
   int32_t n_seg;
   int32_t G;
   float scale_log2;  // scale * log2(e)
@@ -71,12 +78,26 @@ struct AttnParams {
   const int32_t* audio_e;
   int64_t max_audio;
   int32_t Hkv;
+  // APPEND only: the step's rows, the post-append offsets and the capacity
+  // of each segment (rows from base[s] it may occupy)
+  const void* new_k;   // [n_seg, D]
+  const void* new_v;
+  int32_t* cu_out;     // [n_seg + 1], must not alias cu
+  const int32_t* cap;  // [n_seg]
 };
+
+// A segment is attended when its rows fit both row spaces; every piece of
+// logic that decides this (owner outputs, pieces, the stream walk) uses this
+// one test, so all workgroups agree on the segments they skip.
+__device__ __forceinline__ bool seg_valid(int64_t lo, int64_t len, int64_t b, int64_t R, int64_t KV) {
+  return len > 0 && lo >= 0 && lo + len <= R && b >= 0 && b + len <= KV;
+}
 
 // Per-workgroup schedule, shared through LDS.
 struct SchedLds {
-  int64_t R;       // rows partitioned (kv_rows)
-  int64_t B0, B1;  // this workgroup's physical row range
+  int64_t R;       // logical rows partitioned: cu[n_seg] (+ n_seg with APPEND)
+  int64_t KV;      // physical rows (bounds)
+  int64_t B0, B1;  // this workgroup's logical row range
   int32_t P;       // effective number of workgroups (<= R)
   int32_t s_first, s_last;
   int32_t is_last;  // combine flag broadcast
@@ -85,29 +106,60 @@ struct SchedLds {
   // them then skip the split-K hand-off: no arrival counter is touched and
   // the workspace stays valid for the next launch.
   int32_t order_bad;
-  alignas(16) int32_t hdr[16][4];  // streaming kernel: merge slot headers (segment, length, base lo, base hi)
-  int64_t ring_base[kRing];
+  alignas(16) int32_t hdr[16][4];  // streaming kernel: merge slot headers (segment, length, logical start lo, hi)
+  int64_t ring_base[kRing];  // physical first row
+  int32_t ring_lo[kRing];    // logical first row
   int32_t ring_len[kRing];
+  int32_t ring_cap[kRing];   // with APPEND: capacity
   int32_t ring_a0[kRing];    // with xlog: audio start of the segment
   int32_t ring_alen[kRing];  // with xlog: audio rows kept (0: segment not scored)
 };
 
-__device__ __forceinline__ int64_t range_start(int64_t p, int64_t R, int64_t P) {
-  return (p * R) / P;
+// The logical rows [0, R) are split over P workgroups, [floor(p R / P),
+// floor((p + 1) R / P)) for workgroup p, and each workgroup's range over its
+// kSplitWaves waves the same way (unit u = p * kSplitWaves + w of
+// P * kSplitWaves), so wave and workgroup bounds agree.
+static constexpr int kSplitWaves = 4;
+
+// floor(u R / U) for U = gridDim.x * kSplitWaves with inv = ceil(2^64 / U):
+// the high half of u R * inv, exact for n = u R < 2^64 / U (R < 2^32, U <
+// 2^14): the product overshoots n / U by less than n / 2^64 < 1 / U, and
+// the fraction of n / U is at most 1 - 1 / U.
+__device__ __forceinline__ int64_t unit_start(int64_t u, int64_t R, uint64_t inv) {
+  return (int64_t)__umul64hi((uint64_t)(u * R), inv);
 }
-// The workgroup whose row range holds physical row j (P <= R).
+// The workgroup whose row range holds logical row j (P <= R).
 __device__ __forceinline__ int64_t owner_of(int64_t j, int64_t R, int64_t P) {
   return ((j + 1) * P - 1) / R;
 }
 __device__ __forceinline__ int64_t effective_wgs(int64_t R) {
   return R > 0 ? min((int64_t)gridDim.x, R) : 0;
 }
+// Start of split unit u (of P * kSplitWaves) for R rows: the reciprocal
+// when every workgroup of the grid takes part (R >= gridDim.x), else a
+// division (tiny launches).
+__device__ __forceinline__ int64_t split_start(int64_t u, int64_t R, int64_t P, uint64_t inv) {
+  if (P == (int64_t)gridDim.x && inv != 0) return unit_start(u, R, inv);
+  return (u * R) / (P * kSplitWaves);
+}
+// This workgroup's logical row range [B0, B1) for R rows over P workgroups.
+__device__ __forceinline__ void wg_range(int64_t R, int64_t P, uint64_t inv, int64_t& B0, int64_t& B1) {
+  const int64_t pid = blockIdx.x;
+  if (pid >= P) {
+    B0 = B1 = 0;
+    return;
+  }
+  B0 = split_start(pid * kSplitWaves, R, P, inv);
+  B1 = split_start((pid + 1) * kSplitWaves, R, P, inv);
+}
 
 // Workgroup prologue: one pass over cu / base (all threads, independent
-// loads) finds the segments whose rows overlap this workgroup's range,
-// checks the layout, and writes the outputs of empty segments (zeros) and of
-// invalid ones (NaN) owned by this workgroup (segment i -> workgroup i % grid).
-template <typename T, int NT, bool XL = false>
+// loads) finds the segments whose logical rows overlap this workgroup's
+// range, checks the table, and writes the outputs of empty segments (zeros)
+// and of invalid ones (NaN) owned by this workgroup (segment i -> workgroup
+// i % grid).  With APPEND, lengths include the new row and workgroup 0
+// writes cu_out.
+template <typename T, int NT, bool XL = false, bool APPEND = false>
 __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
   const int tid = threadIdx.x;
   const int N = p.n_seg;
@@ -116,14 +168,10 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
     sl.s_last = -1;
     sl.order_bad = 0;
   }
-  const int64_t R = p.kv_rows;
-  const int64_t P = effective_wgs(R);
+  const int64_t KV = p.phys_rows;
   const int64_t pid = blockIdx.x;
-  const bool active = pid < P;
-  const int64_t B0 = active ? range_start(pid, R, P) : 0;
-  const int64_t B1 = active ? range_start(pid + 1, R, P) : 0;
-  int32_t lo[4], hi[4], nxt[4];
-  int64_t bs[4], bn[4];
+  int32_t lo[4], hi[4], cp[4];
+  int64_t bs[4];
   int32_t xm[4], xa[4], xe[4];  // with xlog: KV-head flag, audio range
   const WNW_GLOBAL int32_t* cu = gptr<int32_t>(p.cu);
   const WNW_GLOBAL int64_t* basep = gptr<int64_t>(p.base);
@@ -131,8 +179,8 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * NT + tid;
-      lo[u] = hi[u] = nxt[u] = 0;
-      bs[u] = bn[u] = 0;
+      lo[u] = hi[u] = cp[u] = 0;
+      bs[u] = 0;
       xm[u] = xa[u] = xe[u] = 0;
       if (XL && i < N) {
         xm[u] = gptr<int32_t>(p.xmask)[i % p.Hkv];
@@ -142,12 +190,8 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       if (i < N) {
         lo[u] = cu[i];
         hi[u] = cu[i + 1];
-        if (p.base) {
-          bs[u] = basep[i];
-          if (i + 1 < N) bn[u] = basep[i + 1];
-        } else if (i + 1 < N) {
-          nxt[u] = 1;
-        }
+        if (p.base) bs[u] = basep[i];
+        if (APPEND) cp[u] = gptr<int32_t>(p.cap)[i];
       }
     }
   };
@@ -156,37 +200,48 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   // empty (length 0), not as what an earlier kernel left in LDS.
   if (tid < kRing) {
     sl.ring_base[tid] = 0;
+    sl.ring_lo[tid] = 0;
     sl.ring_len[tid] = 0;
+    sl.ring_cap[tid] = 0;
     if (XL) {
       sl.ring_a0[tid] = 0;
       sl.ring_alen[tid] = 0;
     }
   }
-  // The loads of the first chunk are issued before the barrier: one global
-  // round trip for n_seg <= 4 * NT.
+  // The loads of the first chunk (and of cu[N], the end of the logical rows
+  // the split covers) are issued before the barrier: one global round trip
+  // for n_seg <= 4 * NT.
+  const int32_t cu_end = cu[N];
   load_chunk(0);
   __syncthreads();
+  const int64_t R = max((int64_t)0, (int64_t)cu_end + (APPEND ? N : 0));
+  const int64_t P = effective_wgs(R);
+  const bool active = pid < P;
+  int64_t B0, B1;
+  wg_range(R, P, p.split_inv, B0, B1);
   for (int i0 = 0; i0 < N; i0 += 4 * NT) {
     if (i0 > 0) load_chunk(i0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * NT + tid;
       if (i >= N) continue;
+      if (APPEND && pid == 0) {  // post-append offsets
+        WNW_GLOBAL int32_t* co = gptr_w<int32_t>(p.cu_out);
+        co[i] = lo[u] + i;
+        if (i == N - 1) co[N] = hi[u] + N;
+      }
       int64_t len = (int64_t)hi[u] - lo[u];
       const int64_t b = p.base ? bs[u] : (int64_t)lo[u];
       if (len < 0) {  // corrupt offsets: treated as an empty segment
         raise_device_error(p.err, WNW_DEVERR_ORDER);
         sl.order_bad = 1;
         len = 0;
+      } else if (APPEND) {
+        ++len;
+        if (len > cp[u]) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
       }
-      // layout order: segment i must end before segment i + 1 starts
-      if (p.base && i + 1 < N && b + len > bn[u]) {
-        raise_device_error(p.err, WNW_DEVERR_ORDER);
-        sl.order_bad = 1;
-      }
-      (void)nxt;
       const bool owner = (i % (int)gridDim.x) == (int)pid;
-      if (len == 0 || b < 0 || b + len > R) {
+      if (!seg_valid(lo[u], len, b, R, KV)) {
         if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
         if (owner) {
           const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
@@ -201,11 +256,13 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
         }
         continue;
       }
-      if (active && b < B1 && b + len > B0) {
+      if (active && lo[u] < B1 && lo[u] + len > B0) {
         atomicMin(&sl.s_first, i);
         atomicMax(&sl.s_last, i);
         sl.ring_base[i % kRing] = b;
+        sl.ring_lo[i % kRing] = lo[u];
         sl.ring_len[i % kRing] = (int32_t)len;
+        sl.ring_cap[i % kRing] = cp[u];
         if (XL) {
           sl.ring_a0[i % kRing] = xa[u];
           sl.ring_alen[i % kRing] = xm[u] ? (int32_t)max((int64_t)0, min((int64_t)xe[u] - xa[u], p.max_audio)) : 0;
@@ -215,6 +272,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   }
   if (tid == 0) {
     sl.R = R;
+    sl.KV = KV;
     sl.P = (int32_t)P;
     sl.B0 = B0;
     sl.B1 = B1;
@@ -223,7 +281,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
 }
 
 struct Piece {
-  int64_t seg_base;  // physical first row of the segment
+  int64_t seg_lo;    // logical first row of the segment
   int64_t seg_len;
   int64_t phys;      // physical row of the piece's first row
   int32_t nrows;     // rows in the piece
@@ -241,28 +299,33 @@ __device__ __forceinline__ int64_t uni(int64_t x) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// The MFMA and VALU kernels (no append): segment s's piece of this
+// workgroup's logical range.
 __device__ __forceinline__ Piece make_piece(const AttnParams& p, const SchedLds& sl, int s) {
   Piece pc;
-  int64_t b, len;
+  int64_t b, lo, len;
   if (sl.s_last - sl.s_first < kRing) {
     b = sl.ring_base[s % kRing];
+    lo = sl.ring_lo[s % kRing];
     len = sl.ring_len[s % kRing];
   } else {
-    const int64_t lo = gptr<int32_t>(p.cu)[s], hi = gptr<int32_t>(p.cu)[s + 1];
-    b = p.base ? gptr<int64_t>(p.base)[s] : lo;
-    len = hi - lo;
+    const int64_t c0 = gptr<int32_t>(p.cu)[s], c1 = gptr<int32_t>(p.cu)[s + 1];
+    b = p.base ? gptr<int64_t>(p.base)[s] : c0;
+    lo = c0;
+    len = c1 - c0;
   }
   b = uni(b);
+  lo = uni(lo);
   len = uni(len);
-  pc.seg_base = b;
+  pc.seg_lo = lo;
   pc.seg_len = len;
   // Invalid or empty segments inside [s_first, s_last] are skipped here and
   // handled by their owner in schedule(); the condition matches it exactly.
-  pc.skip = !(len > 0 && b >= 0 && b + len <= uni(sl.R) && b < uni(sl.B1) && b + len > uni(sl.B0));
   const int64_t B0 = uni(sl.B0), B1 = uni(sl.B1);
-  const int64_t a = max(b, B0), e = min(b + len, B1);
-  pc.whole = (a == b) && (e == b + len);
-  pc.phys = a;
+  pc.skip = !(seg_valid(lo, len, b, uni(sl.R), uni(sl.KV)) && lo < B1 && lo + len > B0);
+  const int64_t a = max(lo, B0), e = min(lo + len, B1);
+  pc.whole = (a == lo) && (e == lo + len);
+  pc.phys = b + (a - lo);
   pc.nrows = pc.skip ? 0 : (int32_t)(e - a);
   return pc;
 }
@@ -354,21 +417,21 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
   }
 }
 
-// Pieces (workgroups) of the segment at [seg_base, seg_base + seg_len).
-__device__ __forceinline__ void piece_range(const SchedLds& sl, int64_t seg_base, int64_t seg_len, int64_t& p_first,
+// Pieces (workgroups) of the segment at logical rows [seg_lo, seg_lo + seg_len).
+__device__ __forceinline__ void piece_range(const SchedLds& sl, int64_t seg_lo, int64_t seg_len, int64_t& p_first,
                                             int64_t& p_last) {
   const int64_t R = sl.R, P = sl.P;
-  p_first = min(max(owner_of(seg_base, R, P), (int64_t)0), P - 1);
-  p_last = min(max(owner_of(seg_base + seg_len - 1, R, P), p_first), P - 1);
+  p_first = min(max(owner_of(seg_lo, R, P), (int64_t)0), P - 1);
+  p_last = min(max(owner_of(seg_lo + seg_len - 1, R, P), p_first), P - 1);
 }
 
 // Arrival of this workgroup's partial of segment s (already written with
 // agent-coherent stores and waited for, followed by a barrier): bump the
 // segment's counter and return whether this was the last piece.  One thread.
-__device__ __forceinline__ bool arrive(const AttnParams& p, const SchedLds& sl, int64_t seg_base, int64_t seg_len,
+__device__ __forceinline__ bool arrive(const AttnParams& p, const SchedLds& sl, int64_t seg_lo, int64_t seg_len,
                                       int s) {
   int64_t p_first, p_last;
-  piece_range(sl, seg_base, seg_len, p_first, p_last);
+  piece_range(sl, seg_lo, seg_len, p_first, p_last);
   const int old =
       __hip_atomic_fetch_add(gptr_w<int32_t>(p.counters) + s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return old == (int)(p_last - p_first);
@@ -388,22 +451,22 @@ __device__ __forceinline__ void combine_from(const AttnParams& p, int D, int64_t
 // threads t = 0 .. nt - 1 of the workgroup) and resets the counter for the
 // next launch.  No LDS is used.
 template <typename T>
-__device__ __forceinline__ void combine_segment(const AttnParams& p, int D, const SchedLds& sl, int64_t seg_base,
+__device__ __forceinline__ void combine_segment(const AttnParams& p, int D, const SchedLds& sl, int64_t seg_lo,
                                                 int64_t seg_len, int s, int t, int nt) {
   int64_t p_first, p_last;
-  piece_range(sl, seg_base, seg_len, p_first, p_last);
+  piece_range(sl, seg_lo, seg_len, p_first, p_last);
   combine_from<T>(p, D, p_first, (int)(p_last - p_first + 1), s, t, nt);
 }
 
 // Arrival of this workgroup's partial of segment s followed, on the last
 // arrival, by the merge.  Called by all threads.
 template <typename T, int NT>
-__device__ __forceinline__ void arrive_and_combine(const AttnParams& p, int D, SchedLds& sl, int64_t seg_base,
+__device__ __forceinline__ void arrive_and_combine(const AttnParams& p, int D, SchedLds& sl, int64_t seg_lo,
                                                    int64_t seg_len, int s) {
-  if (threadIdx.x == 0) sl.is_last = !sl.order_bad && arrive(p, sl, seg_base, seg_len, s);
+  if (threadIdx.x == 0) sl.is_last = !sl.order_bad && arrive(p, sl, seg_lo, seg_len, s);
   __syncthreads();
   if (!sl.is_last) return;  // workgroup-uniform
-  combine_segment<T>(p, D, sl, seg_base, seg_len, s, threadIdx.x, NT);
+  combine_segment<T>(p, D, sl, seg_lo, seg_len, s, threadIdx.x, NT);
 }
 
 // Merge the NW wave states in LDS (layout: ml[w][g] = (m, l),
@@ -469,7 +532,7 @@ __device__ __forceinline__ void finish_piece(const AttnParams& p, int D, SchedLd
   }
   wait_vmem();
   __syncthreads();
-  arrive_and_combine<T, NT>(p, D, sl, pc.seg_base, pc.seg_len, s);
+  arrive_and_combine<T, NT>(p, D, sl, pc.seg_lo, pc.seg_len, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -780,6 +843,20 @@ __device__ __forceinline__ void dma_copy16(const void* gbase, uint32_t voff, uin
       : "memory");
 }
 
+// The same copy with a 64-bit address per lane (no scalar base), for a load
+// whose lanes read from two different arrays.
+__device__ __forceinline__ void dma_copy16_a64(const void* gaddr, uint32_t lds_addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(gaddr), "s"(lds_addr)
+      : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -856,29 +933,31 @@ __host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot) {
 
 // One step of a wave's stream: rows [row0, row0 + nrows) of segment s.
 struct SStep {
-  int64_t row0;
-  int64_t seg_b;
+  int64_t row0;    // physical row of the step's first row
+  int64_t seg_lo;  // logical first row of the segment
   int32_t s, nrows, seg_len, qslot;
   int32_t first, last, whole;
   int32_t t0, alen;  // audio index of the first row; audio rows whose logits are kept (0: none)
+  int32_t newrow;    // APPEND: 1 = the step's last row is the segment's new row, 2 = and it is written to the pool
 };
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
-template <typename T, int D, int NW, int QD, bool XL>
+// APPEND: append new_k / new_v[s] to every segment first (fused append).
+template <typename T, int D, int NW, int QD, bool XL, bool APPEND>
 // The fields read first lead the argument list as scalars: the build
 // preloads the first 16 argument dwords into SGPRs at dispatch
 // (-amdgpu-kernarg-preload-count), so the segment table and the first steps
 // are addressed without a kernel-argument load; aggregates are not preloaded.
 __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_arg, const void* k_arg, const void* v_arg,
                                                                const int32_t* cu_arg, const int64_t* base_arg,
-                                                               int64_t rows_arg, int32_t nseg_arg, int32_t g_arg,
+                                                               uint64_t inv_arg, int32_t nseg_arg, int32_t g_arg,
                                                                AttnParams p) {
   p.q = q_arg;
   p.k = k_arg;
   p.v = v_arg;
   p.cu = cu_arg;
   p.base = base_arg;
-  p.kv_rows = rows_arg;
+  p.split_inv = inv_arg;
   p.n_seg = nseg_arg;
   p.G = g_arg;
   using G_ = StreamGeom<D>;
@@ -910,12 +989,26 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   const T* vp = (const T*)p.v;
   // rows [row0, row0 + nrows) of K or V into step buffer b, 16-byte chunks
   // swizzled by the row (K: chunk ^ (r % CH); V: chunk ^ 2 (r % 4)); rows past
-  // nrows repeat the last row
-  auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b) {
+  // nrows repeat the last row.  news >= 0 (APPEND): the last row is segment
+  // news's new row, read from new_k / new_v (the pool does not hold it yet).
+  auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b, int news) {
     // wave-uniform addresses, kept scalar (the load takes them in SGPRs)
     const T* src = (const T*)uni((int64_t)(uintptr_t)((is_v ? vp : kp) + row0 * D));
     const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_w + b * 2 * SB + (is_v ? SB : 0));
     nrows = uni((int32_t)nrows);
+    if (APPEND && news >= 0) {  // wave-uniform; the same number of loads either way
+      const uint8_t* nsrc = (const uint8_t*)(is_v ? p.new_v : p.new_k) + (int64_t)news * RB;
+#pragma unroll
+      for (int u = 0; u < NI; ++u) {
+        const int r = u * RPI + lane / CH;
+        const int rr = max(0, r < nrows ? r : nrows - 1);
+        const int sw = is_v ? 2 * (r & 3) : r % CH;
+        const int chunk = ((lane % CH) ^ sw) * 16;
+        const uint8_t* a = rr == nrows - 1 ? nsrc + chunk : (const uint8_t*)src + rr * RB + chunk;
+        dma_copy16_a64(a, dst + u * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int r = u * RPI + lane / CH;
@@ -930,24 +1023,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   // invalid segments) follow once those loads are out.  More segments: the
   // workgroup pass of schedule() first, with its LDS cache of the bounds.
   const bool direct = p.n_seg <= 64;
-  int64_t R, B0, B1;
+  const int64_t KV = p.phys_rows;
+  int64_t R = 0, B0 = 0, B1 = 0;
   int s_first, s_last;
-  if (direct) {
-    R = p.kv_rows;
-    const int64_t P = effective_wgs(R);
-    const bool active = (int64_t)blockIdx.x < P;
-    B0 = active ? range_start(blockIdx.x, R, P) : 0;
-    B1 = active ? range_start(blockIdx.x + 1, R, P) : 0;
+  if (direct) {  // the split range follows from the table (below)
     s_first = 0;
     s_last = p.n_seg - 1;
-    if (tid == 0) {  // read by the merge and the hand-off, after barriers
-      sl.R = R;
-      sl.P = (int32_t)P;
-      sl.B0 = B0;
-      sl.B1 = B1;
-    }
   } else {
-    schedule<T, NT, XL>(p, D, sl);
+    schedule<T, NT, XL, APPEND>(p, D, sl);
     if (sl.s_first > sl.s_last) return;
     R = uni(sl.R);
     B0 = uni(sl.B0);
@@ -955,24 +1038,42 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     s_first = uni(sl.s_first);
     s_last = uni(sl.s_last);
   }
-  const int64_t W0 = B0 + (B1 - B0) * w / NW, W1 = B0 + (B1 - B0) * (w + 1) / NW;
+  static_assert(NW == kSplitWaves, "wave ranges are units of the split");
+  int64_t P_ = direct ? 0 : (int64_t)uni(sl.P);
+  int64_t W0 = 0, W1 = 0;
+  if (!direct && (int64_t)blockIdx.x < P_) {
+    W0 = split_start((int64_t)blockIdx.x * NW + w, R, P_, p.split_inv);
+    W1 = split_start((int64_t)blockIdx.x * NW + w + 1, R, P_, p.split_inv);
+  }
   const bool in_ring = !direct && (s_last - s_first) < kRing;
 
   // ---- segment walk: a window of 64 segments, one per lane; the mask holds
   // the valid ones overlapping [W0, W1) that are not taken yet.
   int wb = s_first;
-  int64_t lb = 0;
-  int32_t llen = 0, la0 = 0, lal = 0;
+  int64_t lb = 0;  // physical first row
+  int32_t llo = 0, llen = 0, lcap = 0, la0 = 0, lal = 0;  // logical first row, length, capacity
+  bool lneg = false;  // the offsets of this lane's segment decrease
   uint64_t mask = 0;
-  auto load_window = [&]() {
+  // the segments of the window that overlap this wave's range [W0, W1)
+  auto window_mask = [&]() {
+    // the piece [max(lo, W0), min(lo + len, W1)) must be non-empty (an empty
+    // wave range inside a segment overlaps nothing)
+    const bool ov = wb + lane <= s_last && seg_valid(llo, llen, lb, R, KV) &&
+                    max((int64_t)llo, W0) < min((int64_t)llo + llen, W1);
+    mask = __ballot(ov);
+  };
+  auto load_window = [&](bool with_mask) {
     const int s = wb + lane;
     lb = 0;
-    llen = 0;
+    llo = llen = lcap = 0;
     la0 = lal = 0;
+    lneg = false;
     if (s <= s_last) {
       if (in_ring) {
         lb = sl.ring_base[s % kRing];
+        llo = sl.ring_lo[s % kRing];
         llen = sl.ring_len[s % kRing];
+        if (APPEND) lcap = sl.ring_cap[s % kRing];
         if (XL) {
           la0 = sl.ring_a0[s % kRing];
           lal = sl.ring_alen[s % kRing];
@@ -980,22 +1081,40 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       } else {
         const int32_t lo = p.cu[s], hi = p.cu[s + 1];
         lb = p.base ? p.base[s] : (int64_t)lo;
+        llo = lo;
         llen = hi - lo;
+        lneg = llen < 0;
+        if (APPEND) {
+          lcap = p.cap[s];
+          if (!lneg) ++llen;
+        }
         if (XL && p.xmask[s % p.Hkv]) {
           la0 = p.audio_s[s / p.Hkv];
           lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
         }
       }
     }
-    // the piece [max(lb, W0), min(lb + len, W1)) must be non-empty (an empty
-    // wave range inside a segment overlaps nothing)
-    const bool ov = s <= s_last && llen > 0 && lb >= 0 && lb + llen <= R && max(lb, W0) < min(lb + llen, W1);
-    mask = __ballot(ov);
+    if (with_mask) window_mask();
   };
-  load_window();
-  // issue-side iterator: current piece [pb, pe) of segment cur_s
-  int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0;
-  int64_t cur_b = 0, pb = 0, pe = 0, irow = 0;
+  load_window(!direct);
+  if (direct) {
+    // The rows the split covers end at cu[n_seg] (+ n_seg with APPEND):
+    // lane n_seg - 1 holds it.  Read from the table rather than passed in,
+    // so a launch captured in a graph stays right as the segments grow.
+    // Only this wave's own bounds sit on the start-up path; the
+    // workgroup's follow once the first steps are issued.
+    const int32_t lhi = APPEND && !lneg ? llo + llen - 1 : llo + llen;  // cu[s + 1]
+    R = max((int64_t)0, (int64_t)__builtin_amdgcn_readlane(lhi, p.n_seg - 1) + (APPEND ? p.n_seg : 0));
+    P_ = effective_wgs(R);
+    if ((int64_t)blockIdx.x < P_) {
+      W0 = split_start((int64_t)blockIdx.x * NW + w, R, P_, p.split_inv);
+      W1 = split_start((int64_t)blockIdx.x * NW + w + 1, R, P_, p.split_inv);
+    }
+    window_mask();
+  }
+  // issue-side iterator: current piece [pb, pe) of segment cur_s (logical rows)
+  int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0, cur_wr = 0;
+  int64_t cur_b = 0, cur_lo = 0, pb = 0, pe = 0, irow = 0;
   bool cur_whole = false, have = false;
   auto next_piece = [&]() {
     while (mask == 0) {
@@ -1004,7 +1123,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
         have = false;
         return;
       }
-      load_window();
+      load_window(true);
     }
     const int k = __builtin_ctzll(mask);
     mask &= mask - 1;
@@ -1012,14 +1131,16 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     const uint32_t blo = __builtin_amdgcn_readlane((uint32_t)lb, k);
     const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)lb >> 32), k);
     cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
+    cur_lo = __builtin_amdgcn_readlane(llo, k);
     cur_len = __builtin_amdgcn_readlane(llen, k);
+    if (APPEND) cur_wr = cur_len <= __builtin_amdgcn_readlane(lcap, k) ? 2 : 1;
     if (XL) {
       cur_a0 = __builtin_amdgcn_readlane(la0, k);
       cur_al = __builtin_amdgcn_readlane(lal, k);
     }
-    pb = max(cur_b, W0);
-    pe = min(cur_b + cur_len, W1);
-    cur_whole = cur_b >= W0 && cur_b + cur_len <= W1;
+    pb = max(cur_lo, W0);
+    pe = min(cur_lo + cur_len, W1);
+    cur_whole = cur_lo >= W0 && cur_lo + cur_len <= W1;
     irow = pb;
     have = true;
   };
@@ -1027,17 +1148,18 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   auto gen = [&](SStep& st) -> bool {
     if (!have) return false;
     st.s = cur_s;
-    st.seg_b = cur_b;
+    st.seg_lo = cur_lo;
     st.seg_len = cur_len;
-    st.row0 = irow;
+    st.row0 = cur_b + (irow - cur_lo);
     st.nrows = (int32_t)min((int64_t)kSRows, pe - irow);
     st.first = irow == pb;
     st.whole = cur_whole;
     st.qslot = piece_no & 1;
     if (XL) {
-      st.t0 = (int32_t)(irow - cur_b) - cur_a0;
+      st.t0 = (int32_t)(irow - cur_lo) - cur_a0;
       st.alen = cur_al;
     }
+    st.newrow = APPEND && irow + st.nrows == cur_lo + cur_len ? cur_wr : 0;
     irow += kSRows;
     st.last = irow >= pe;
     if (st.last) {
@@ -1051,7 +1173,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   // q is loaded for the first step of a piece only (the later steps keep it
   // in registers), so a step issues E loads with q and E - QD without.
   auto issue = [&](const SStep& st, int b) {
-    load_rows(false, st.row0, st.nrows, b);
+    load_rows(false, st.row0, st.nrows, b, st.newrow ? st.s : -1);
     if (st.first) {
       const T* qs = (const T*)uni((int64_t)(uintptr_t)((const T*)p.q + (int64_t)st.s * G * D));
 #pragma unroll
@@ -1061,7 +1183,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
           dma_copy16(qs, (uint32_t)off, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + u * 1024));
       }
     }
-    load_rows(true, st.row0, st.nrows, b);
+    load_rows(true, st.row0, st.nrows, b, st.newrow ? st.s : -1);
   };
 
   // ---- softmax state of the current piece, and the held (first, shared) one
@@ -1167,6 +1289,21 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (APPEND && st.newrow == 2) {
+      // the segment's new row (the step's last row, read from new_k / new_v)
+      // goes into the pool from LDS: lanes 0 .. CH-1 write its K chunks,
+      // CH .. 2CH-1 its V chunks (un-swizzled); no other wave reads that
+      // pool row in this launch
+      const int r = st.nrows - 1;
+      if (lane < 2 * CH) {
+        const bool isv = lane >= CH;
+        const int c = lane % CH;
+        const int sw = isv ? 2 * (r & 3) : r % CH;
+        const u32x4 d = *(const u32x4*)((isv ? vbuf : kbuf) + r * RB + (c ^ sw) * 16);
+        WNW_GLOBAL uint8_t* dst = gptr_w<uint8_t>(const_cast<void*>(isv ? p.v : p.k)) + (st.row0 + r) * RB + c * 16;
+        *(WNW_GLOBAL u32x4*)dst = d;
+      }
+    }
     if (st.last) {
       const float l_tot = sum_x32(sum_x16(l_run));
       if (st.whole) {  // the segment lies inside this wave's range: finish it
@@ -1188,7 +1325,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
         }
       } else if (h_s < 0) {  // first shared piece: hold it until the end
         h_s = st.s;
-        h_b = st.seg_b;
+        h_b = st.seg_lo;
         h_len = st.seg_len;
         m_h = m_run;
         l_h = l_tot;
@@ -1196,7 +1333,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
         for (int t = 0; t < NTD; ++t) acc_h[t] = acc[t];
       } else {  // last shared piece: it is the end of this wave's range
         c_s = st.s;
-        c_b = st.seg_b;
+        c_b = st.seg_lo;
         c_len = st.seg_len;
         l_run = l_tot;
         return;
@@ -1214,23 +1351,39 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   if (hA) issue(sA, 0);
   bool hB = hA && gen(sB);
   if (hB) issue(sB, 1);
+  if (direct) {
+    wg_range(R, P_, p.split_inv, B0, B1);
+    if (tid == 0) {  // read by the merge and the hand-off, after barriers
+      sl.R = R;
+      sl.KV = KV;
+      sl.P = (int32_t)P_;
+      sl.B0 = B0;
+      sl.B1 = B1;
+    }
+  }
   // direct: the checks of schedule() from the table window in registers
   // (lane i holds segment i; no new loads, which would wait behind the
   // steps just issued).  Wave 0 of every workgroup; the outputs of empty
   // and invalid segments are written by workgroup i % grid.
   if (direct && w == 0) {
-    // base of segment lane + 1 (read with every lane active)
-    const uint32_t nlo = __shfl_down((uint32_t)lb, 1), nhi = __shfl_down((uint32_t)((uint64_t)lb >> 32), 1);
-    const int64_t nb = (int64_t)(((uint64_t)nhi << 32) | nlo);
     const int si = lane;
-    int64_t len = si < p.n_seg ? llen : 0;
-    const bool neg = len < 0;
-    if (neg) len = 0;  // corrupt offsets: treated as an empty segment
-    const bool bad = neg || (p.base && si + 1 < p.n_seg && lb + len > nb);
+    const bool in = si < p.n_seg;
+    // llen already counts the new row with APPEND, unless the offsets
+    // decrease (lneg: a corrupt table, treated as an empty segment)
+    const int64_t len = in && !lneg ? llen : 0;
+    const bool bad = in && lneg;
     if (bad) raise_device_error(p.err, WNW_DEVERR_ORDER);
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) sl.order_bad = any_bad;
-    if (si < p.n_seg && (len == 0 || lb < 0 || lb + len > R)) {
+    if (APPEND && in) {
+      if (!lneg && len > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
+      if (blockIdx.x == 0) {  // post-append offsets: cu_out = cu + arange(n_seg + 1)
+        WNW_GLOBAL int32_t* co = gptr_w<int32_t>(p.cu_out);
+        co[si] = llo + si;
+        if (si == p.n_seg - 1) co[p.n_seg] = llo + llen - (lneg ? 0 : 1) + p.n_seg;
+      }
+    }
+    if (in && !seg_valid(llo, len, lb, R, KV)) {
       if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
       if ((si % (int)gridDim.x) == (int)blockIdx.x) {
         const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
@@ -1652,18 +1805,27 @@ static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex&
 // Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
 // stream_lds_bytes (above 64 KB, so the limit is raised once per instance
 // and device).
-template <typename T, int D, int QD, bool XL>
+template <typename T, int D, int QD, bool XL, bool APPEND>
 static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
   const int qslot = (ap.G * D * 2 + 255) & ~255;
   const int lds = stream_lds_bytes(D, kNW, qslot);
   static std::mutex mu;
   static std::vector<signed char> done;
-  const hipError_t attr_err = set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL>,
-                                                 stream_lds_bytes(D, kNW, 2048));
+  const hipError_t attr_err = set_lds_limit_once(
+      done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND>, stream_lds_bytes(D, kNW, 2048));
   if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL>), dim3((unsigned)n_wg), dim3(kNW * 64), lds, st, ap.q,
-                     ap.k, ap.v, ap.cu, ap.base, ap.kv_rows, ap.n_seg, ap.G, ap);
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
+                     st, ap.q, ap.k, ap.v, ap.cu, ap.base, ap.split_inv, ap.n_seg, ap.G, ap);
   return hipGetLastError();
+}
+
+template <typename T, int D, int QD>
+static hipError_t launch_stream_qd(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+  if (ap.new_k)
+    return ap.xlog ? launch_stream<T, D, QD, true, true>(ap, n_wg, st)
+                   : launch_stream<T, D, QD, false, true>(ap, n_wg, st);
+  return ap.xlog ? launch_stream<T, D, QD, true, false>(ap, n_wg, st)
+                 : launch_stream<T, D, QD, false, false>(ap, n_wg, st);
 }
 
 template <typename T, int D>
@@ -1672,9 +1834,9 @@ static hipError_t launch_attn(int kernel, const AttnParams& ap, int64_t n_wg, hi
     if constexpr (sizeof(T) == 2 && (D == 64 || D == 128)) {
       const int qd = (ap.G * D * 2 + 1023) / 1024;
       if (ap.G <= kMaxGroupS) {
-        if (ap.xlog)
-          return qd == 1 ? launch_stream<T, D, 1, true>(ap, n_wg, st) : launch_stream<T, D, 2, true>(ap, n_wg, st);
-        return qd == 1 ? launch_stream<T, D, 1, false>(ap, n_wg, st) : launch_stream<T, D, 2, false>(ap, n_wg, st);
+        if constexpr (D == 128)
+          if (qd == 2) return launch_stream_qd<T, D, 2>(ap, n_wg, st);
+        if (qd == 1) return launch_stream_qd<T, D, 1>(ap, n_wg, st);
       }
     }
     return hipErrorInvalidValue;
@@ -1753,7 +1915,8 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                      const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc) {
+                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc,
+                     const AttnAppend* app) {
   if (logits_kept) *logits_kept = 0;
   WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1ll << 30), "n_seg out of range: %lld", (long long)n_seg);
   if (n_seg == 0) return WNW_OK;
@@ -1765,6 +1928,13 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                 "head_dim must be 64, 128 or 256, got %lld", (long long)head_dim);
   WNW_CHECK_ARG(dtype == WNW_F32 || dtype == WNW_F16 || dtype == WNW_BF16, "bad dtype %d", dtype);
   WNW_CHECK_ARG(total_rows >= 0 && kv_rows >= 0, "negative row count");
+  if (app) {
+    WNW_CHECK_ARG(seg_base && app->new_k && app->new_v && app->cu_out && app->cap,
+                  "the fused append needs seg_base, new rows, cu_out and seg_cap");
+    WNW_CHECK_ARG((const void*)app->cu_out != (const void*)cu_k, "cu_out must not alias cu");
+    WNW_CHECK_ARG(((uintptr_t)app->new_k % 16) == 0 && ((uintptr_t)app->new_v % 16) == 0,
+                  "new_k and new_v must be 16-byte aligned");
+  }
   WNW_CHECK_ARG(kv_rows < (1ll << 40), "kv_rows too large");
   WNW_CHECK_ARG(((uintptr_t)q % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
                     ((uintptr_t)out % 16) == 0,
@@ -1789,7 +1959,7 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
     // one workgroup per CU for the streaming kernel (its four waves keep
     // enough loads in flight, and fewer workgroups mean fewer partials to
     // merge), two per CU for the others.
-    const int64_t by_rows = std::max<int64_t>(1, (kv_rows + 63) / 64);
+    const int64_t by_rows = std::max<int64_t>(1, (total_rows + 63) / 64);
     P = std::min<int64_t>((int64_t)di.cus * (kern == WNW_ATTN_STREAM ? 1 : 2), by_rows);
   }
   P = std::max<int64_t>(1, std::min<int64_t>(P, di.max_wg));
@@ -1822,7 +1992,8 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   ap.part_ml = (float*)((char*)workspace + L.ml);
   ap.part_acc = (float*)((char*)workspace + L.acc);
   ap.err = device_error_word();
-  ap.kv_rows = kv_rows;
+  ap.split_inv = ~0ull / (uint64_t)(P * kSplitWaves) + 1;  // ceil(2^64 / (P * kSplitWaves))
+  ap.phys_rows = kv_rows;
   ap.n_seg = (int32_t)n_seg;
   ap.G = (int32_t)group;
   ap.scale_log2 = scale * kLog2e;
@@ -1830,6 +2001,23 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   ap.xmask = ap.audio_s = ap.audio_e = nullptr;
   ap.max_audio = 0;
   ap.Hkv = 1;
+  ap.new_k = ap.new_v = nullptr;
+  ap.cu_out = nullptr;
+  ap.cap = nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  if (app) {
+    if (kern == WNW_ATTN_STREAM) {  // fused into the launch
+      ap.new_k = app->new_k;
+      ap.new_v = app->new_v;
+      ap.cu_out = app->cu_out;
+      ap.cap = app->cap;
+    } else {  // the in-place append first, then attention over the new offsets
+      const int rc = wnw_append_inplace(const_cast<void*>(k), const_cast<void*>(v), app->new_k, app->new_v, cu_k,
+                                        app->cu_out, seg_base, app->cap, n_seg, kv_rows, head_dim, dtype, stream);
+      if (rc != WNW_OK) return rc;
+      ap.cu = app->cu_out;
+    }
+  }
   if (logits && kern == WNW_ATTN_STREAM) {
     WNW_CHECK_ARG(logits->xlog && logits->mask && logits->audio_s && logits->audio_e, "null logits argument");
     WNW_CHECK_ARG(logits->hkv >= 1 && n_seg % logits->hkv == 0 && logits->max_audio > 0,
@@ -1842,7 +2030,6 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
     ap.Hkv = logits->hkv;
     if (logits_kept) *logits_kept = 1;
   }
-  hipStream_t st = (hipStream_t)stream;
   hipError_t e = hipErrorInvalidValue;
   switch (dtype) {
     case WNW_BF16: e = launch_attn_d<bf16_t>(kern, head_dim, ap, P, st); break;
@@ -1862,7 +2049,7 @@ extern "C" int wnw_decode_attn_ex(const void* q, const void* k, const void* v, c
                                   int kernel, int64_t n_wg, void* stream) {
   return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
                           dtype, out, workspace, workspace_bytes, kernel, n_wg, nullptr, nullptr, nullptr,
-                          stream, false);
+                          stream, false, nullptr);
 }
 
 extern "C" int wnw_decode_attn(const void* q, const void* k, const void* v, const int32_t* cu_k,
@@ -1879,5 +2066,22 @@ extern "C" int wnw_decode_attn_noalloc(const void* q, const void* k, const void*
                                        int64_t head_dim, int64_t total_rows, int64_t kv_rows, float scale,
                                        int dtype, void* out, void* stream) {
   return decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
-                          dtype, out, nullptr, 0, WNW_ATTN_AUTO, 0, nullptr, nullptr, nullptr, stream, true);
+                          dtype, out, nullptr, 0, WNW_ATTN_AUTO, 0, nullptr, nullptr, nullptr, stream, true,
+                          nullptr);
+}
+
+extern "C" int wnw_decode_attn_append(const void* q, void* k_pool, void* v_pool, const void* new_k,
+                                      const void* new_v, const int32_t* cu_old, int32_t* cu_new,
+                                      const int64_t* seg_base, const int32_t* seg_cap, int64_t n_seg,
+                                      int64_t group, int64_t head_dim, int64_t total_rows, int64_t pool_rows,
+                                      float scale, int dtype, void* out, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  AttnAppend app;
+  app.new_k = new_k;
+  app.new_v = new_v;
+  app.cu_out = cu_new;
+  app.cap = seg_cap;
+  return decode_attn_impl(q, k_pool, v_pool, cu_old, seg_base, n_seg, group, head_dim, total_rows, pool_rows,
+                          scale, dtype, out, workspace, workspace_bytes, WNW_ATTN_AUTO, 0, nullptr, nullptr,
+                          nullptr, stream, false, &app);
 }

@@ -426,14 +426,14 @@ extern "C" int64_t wnw_decode_attn_score_workspace_bytes(int64_t n_seg, int64_t 
   return score_logits_offset(a, n_seg, group) + up256(n_seg * group * max_audio * 4);
 }
 
-extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v, const int32_t* cu_k,
-                                     const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
-                                     int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
-                                     const int32_t* ca_kv_mask, int64_t num_kv_heads,
-                                     const int32_t* audio_starts, const int32_t* audio_ends,
-                                     float* score_acc, const int32_t* score_offsets, int64_t acc_len,
-                                     int64_t max_audio, void* workspace, int64_t workspace_bytes,
-                                     void* stream) {
+// Attention (with the step's append when app is given) + class-A scoring.
+static int decode_attn_score_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                                  const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
+                                  int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
+                                  const int32_t* ca_kv_mask, int64_t num_kv_heads, const int32_t* audio_starts,
+                                  const int32_t* audio_ends, float* score_acc, const int32_t* score_offsets,
+                                  int64_t acc_len, int64_t max_audio, void* workspace, int64_t workspace_bytes,
+                                  void* stream, const AttnAppend* app) {
   WNW_CHECK_ARG(num_kv_heads >= 1 && n_seg % num_kv_heads == 0,
                 "n_seg (%lld) must be a multiple of num_kv_heads (%lld)", (long long)n_seg,
                 (long long)num_kv_heads);
@@ -459,13 +459,14 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   int kept = 0;
   int rc = decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
                             dtype, out, workspace, attn_ws, WNW_ATTN_AUTO, 0, lse, room ? &lg : nullptr, &kept,
-                            stream, false);
+                            stream, false, app);
   if (rc != WNW_OK || n_seg == 0 || max_audio == 0) return rc;
+  const int32_t* cu_scored = app ? app->cu_out : cu_k;  // the segments as the attention saw them
   if (kept) {
     LogitScoreParams lp;
     lp.xlog = lg.xlog;
     lp.lse = lse;
-    lp.cu = cu_k;
+    lp.cu = cu_scored;
     lp.base = seg_base;
     lp.mask = ca_kv_mask;
     lp.audio_s = audio_starts;
@@ -487,7 +488,7 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   AttnScoreParams sp;
   sp.q = q;
   sp.k = k;
-  sp.cu = cu_k;
+  sp.cu = cu_scored;
   sp.base = seg_base;
   sp.lse = lse;
   sp.mask = ca_kv_mask;
@@ -508,6 +509,36 @@ extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v
   WNW_CHECK_HIP(launch_score(kAttnScore, dtype, head_dim, iters, grid, sp, (hipStream_t)stream),
                 "attention score launch");
   return WNW_OK;
+}
+
+extern "C" int wnw_decode_attn_score(const void* q, const void* k, const void* v, const int32_t* cu_k,
+                                     const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
+                                     int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
+                                     const int32_t* ca_kv_mask, int64_t num_kv_heads,
+                                     const int32_t* audio_starts, const int32_t* audio_ends,
+                                     float* score_acc, const int32_t* score_offsets, int64_t acc_len,
+                                     int64_t max_audio, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  return decode_attn_score_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale, dtype,
+                                out, ca_kv_mask, num_kv_heads, audio_starts, audio_ends, score_acc, score_offsets,
+                                acc_len, max_audio, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int wnw_decode_attn_score_append(
+    const void* q, void* k_pool, void* v_pool, const void* new_k, const void* new_v, const int32_t* cu_old,
+    int32_t* cu_new, const int64_t* seg_base, const int32_t* seg_cap, int64_t n_seg, int64_t group,
+    int64_t head_dim, int64_t total_rows, int64_t pool_rows, float scale, int dtype, void* out,
+    const int32_t* ca_kv_mask, int64_t num_kv_heads, const int32_t* audio_starts, const int32_t* audio_ends,
+    float* score_acc, const int32_t* score_offsets, int64_t acc_len, int64_t max_audio, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  AttnAppend app;
+  app.new_k = new_k;
+  app.new_v = new_v;
+  app.cu_out = cu_new;
+  app.cap = seg_cap;
+  return decode_attn_score_impl(q, k_pool, v_pool, cu_old, seg_base, n_seg, group, head_dim, total_rows, pool_rows,
+                                scale, dtype, out, ca_kv_mask, num_kv_heads, audio_starts, audio_ends, score_acc,
+                                score_offsets, acc_len, max_audio, workspace, workspace_bytes, stream, &app);
 }
 
 extern "C" int64_t wnw_fused_score_workspace_bytes(int64_t n_samples, int64_t n_heads) {

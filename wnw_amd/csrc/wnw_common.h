@@ -31,15 +31,28 @@ struct AttnLogits {
   int32_t hkv;
 };
 
+// The step's append of one row per segment, done before the attention reads
+// the segments: fused into the streaming kernel, else by the in-place append
+// kernel first.  Needs a slack layout (seg_base).
+struct AttnAppend {
+  const void* new_k;   // [n_seg, D]
+  const void* new_v;
+  int32_t* cu_out;     // [n_seg + 1] = cu + arange(n_seg + 1); must not alias cu
+  const int32_t* cap;  // [n_seg] rows each segment may occupy from its base
+};
+
 // Shared by the public attention entry points; lse (optional) receives each
 // segment's final softmax (max, sum) in the log2 domain, [n_seg, G, 2].
 // logits (optional) is honoured by the streaming kernel only; *logits_kept
-// (optional) tells whether they were written.
+// (optional) tells whether they were written.  total_rows = the logical rows
+// the work split covers (after the append, with app).  noalloc: use the
+// library's own scratch instead of the workspace argument.
 int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t* cu_k,
                      const int64_t* seg_base, int64_t n_seg, int64_t group, int64_t head_dim,
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
-                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc);
+                     const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc,
+                     const AttnAppend* app);
 
 #define WNW_CHECK_ARG(cond, ...)       \
   do {                                 \

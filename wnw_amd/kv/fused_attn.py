@@ -83,12 +83,23 @@ def decode_attn(
     workspace: AttnWorkspace | None = None,
     kernel: str = "auto",
     n_wg: int = 0,
+    append: tuple | None = None,
 ) -> torch.Tensor:
     """Decode attention with the layout extensions of this package.
 
     ``seg_base`` (int64 [N]) gives each segment's physical first row in
-    ``k_flat``/``v_flat`` (slack layout); ``total_rows`` is an upper bound of
-    ``cu_k[-1]`` (defaults to ``k_flat.shape[0]``, exact for the dense layout).
+    ``k_flat``/``v_flat`` (slack layout: segments anywhere, in any order).
+    The kernel splits the logical rows ``[0, cu_k[-1])`` over its
+    workgroups, reading ``cu_k[-1]`` on the device; ``total_rows``, an
+    estimate of it, only sizes the grid (required with ``seg_base``; without
+    it the dense layout's ``k_flat.shape[0]``).
+
+    ``append=(new_k [N, D], new_v, cu_new int32 [N+1], seg_cap int32 [N])``
+    first appends one row per segment in place (``k_flat``/``v_flat`` are the
+    pools, ``cu_k`` the offsets before the append, ``total_rows`` an estimate
+    of the rows after it) and attends over the appended segments; the
+    streaming kernel does both in one launch.  ``cu_new`` receives
+    ``cu_k + arange(N + 1)``.
     """
     _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, seg_base)
     if q_flat.dim() != 3:
@@ -102,6 +113,8 @@ def decode_attn(
         raise _lib.WnwError("cu_k must be int32 [N+1]")
     if seg_base is not None and (seg_base.dtype != torch.int64 or seg_base.numel() != nseg):
         raise _lib.WnwError("seg_base must be int64 [N]")
+    if seg_base is not None and total_rows is None:
+        raise _lib.WnwError("total_rows (cu_k[-1]) is required with seg_base")
     if k_flat.shape[0] > 0 and (k_flat.stride(1) != 1 or k_flat.stride(0) != d or v_flat.stride(1) != 1
                                 or v_flat.stride(0) != d):
         raise _lib.WnwError("k_flat / v_flat rows must be contiguous [rows, D]")
@@ -113,11 +126,38 @@ def decode_attn(
     _lib.ensure_init(q_flat.device)
     ws = workspace if workspace is not None else workspace_for(q_flat.device)
     buf, nbytes = ws.get(nseg, g, d)
+    if append is not None:
+        if kernel != "auto" or n_wg:
+            raise _lib.WnwError("the fused append runs the AUTO kernel choice and grid")
+        new_k, new_v, cu_new, seg_cap = _check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base)
+        _lib.check(_lib.lib().wnw_decode_attn_append(
+            _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
+            _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, rows, k_flat.shape[0], float(scale),
+            _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(buf), nbytes, _lib.stream_of(q_flat.device)),
+            "decode_attn_append")
+        return out
     _lib.check(_lib.lib().wnw_decode_attn_ex(
         _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base),
         nseg, g, d, rows, k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out),
         _lib.ptr(buf), nbytes, _KERNELS[kernel], int(n_wg), _lib.stream_of(q_flat.device)), "decode_attn")
     return out
+
+
+def _check_append(append, nseg: int, d: int, dtype, cu_k, seg_base):
+    """Validate the (new_k, new_v, cu_new, seg_cap) of a fused append."""
+    if seg_base is None:
+        raise _lib.WnwError("the fused append needs a slack layout (seg_base)")
+    new_k, new_v, cu_new, seg_cap = append
+    _lib.require_gpu(new_k, new_v, cu_new, seg_cap)
+    if new_k.shape != (nseg, d) or new_v.shape != (nseg, d) or new_k.dtype != dtype or new_v.dtype != dtype:
+        raise _lib.WnwError(f"new_k / new_v must be [{nseg}, {d}] of the pools' dtype")
+    if cu_new.dtype != torch.int32 or cu_new.numel() != nseg + 1 or not cu_new.is_contiguous():
+        raise _lib.WnwError("cu_new must be a contiguous int32 [N+1]")
+    if cu_new.data_ptr() == cu_k.data_ptr():
+        raise _lib.WnwError("cu_new must not alias cu_k")
+    if seg_cap.dtype != torch.int32 or seg_cap.numel() != nseg:
+        raise _lib.WnwError("seg_cap must be int32 [N]")
+    return new_k.contiguous(), new_v.contiguous(), cu_new, seg_cap.contiguous()
 
 
 def q1_decode_attn(
@@ -158,6 +198,7 @@ def q1_decode_attn_score(
     out: torch.Tensor | None = None,
     workspace: AttnWorkspace | None = None,
     keep_logits: bool = True,
+    append: tuple | None = None,
 ) -> torch.Tensor:
     """Attention output [nseg, G, D] plus class-A score accumulation.
 
@@ -170,7 +211,9 @@ def q1_decode_attn_score(
     not given it is read back from the device (one synchronisation).
     ``keep_logits`` lets the attention kernel keep the logits of the scored
     rows for the scoring pass (workspace of n_seg * G * max_audio floats);
-    without it the scoring pass reads the K rows again.
+    without it the scoring pass reads the K rows again.  ``append`` as for
+    ``decode_attn``: the step's rows are appended in place first (scores
+    then cover the appended segments).
     """
     del block_n
     _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_accumulator,
@@ -191,6 +234,8 @@ def q1_decode_attn_score(
         raise _lib.WnwError("cu_k must be int32 [N+1]")
     if max_audio is None:
         max_audio = int((audio_ends - audio_starts).max().item()) if audio_ends.numel() else 0
+    if seg_base is not None and total_rows is None:
+        raise _lib.WnwError("total_rows (cu_k[-1]) is required with seg_base")
     q_flat, cu_k = q_flat.contiguous(), cu_k.contiguous()
     ca_kv_mask, audio_starts, audio_ends, score_offsets = (
         t.contiguous() for t in (ca_kv_mask, audio_starts, audio_ends, score_offsets))
@@ -200,6 +245,16 @@ def q1_decode_attn_score(
     _lib.ensure_init(q_flat.device)
     ws = workspace if workspace is not None else workspace_for(q_flat.device)
     buf, nbytes = ws.get(nseg, g, d, score=True, max_audio=int(max_audio) if keep_logits else 0)
+    if append is not None:
+        new_k, new_v, cu_new, seg_cap = _check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base)
+        _lib.check(_lib.lib().wnw_decode_attn_score_append(
+            _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
+            _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, rows, k_flat.shape[0], float(scale),
+            _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(ca_kv_mask), int(num_kv_heads),
+            _lib.ptr(audio_starts), _lib.ptr(audio_ends), _lib.ptr(score_accumulator), _lib.ptr(score_offsets),
+            score_accumulator.numel(), int(max_audio), _lib.ptr(buf), nbytes, _lib.stream_of(q_flat.device)),
+            "q1_decode_attn_score (append)")
+        return out
     _lib.check(_lib.lib().wnw_decode_attn_score(
         _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base), nseg, g, d, rows,
         k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(ca_kv_mask),
