@@ -3,29 +3,35 @@
 
 Workload (default ``--config cfg2``): Voxtral-Mini-3B decode shape, 30 layers,
 32 query / 8 KV heads, head_dim 128, bf16, batch 8, 7,500 audio + 64 text
-tokens per sequence; per layer 2 of 8 KV heads are class A (full KV), the
-others class B (512 rows).  Synthetic data: K, V ~ N(0, 1) times a
-per-(layer, KV head) scale from U(0.5, 2), q ~ N(0, 1).
+tokens per sequence; per layer 2 of 8 KV heads are class A (full KV, 7,564
+rows), the others class B (512 rows).  Synthetic data: K, V ~ N(0, 1) times
+a per-(layer, KV head) scale from U(0.5, 2), q ~ N(0, 1).
 
-One step = for each of the 30 layers: in-place append of the step's K/V row
-to every segment (slack layout) + split-K decode attention.  All 30 layers
-have distinct buffers (~2.2 GB), far beyond the 256 MB Infinity Cache.  Each
-step is captured once as a HIP graph (two graphs: even/odd step, for the
-ping-ponged offsets) so the timed region measures the GPU, not Python.
+The step runs through the drop-in: a ``WnWCache`` (slack layout) holding
+that state, driven per layer by ``wnw_amd.wnw.session.decode_attention``
+(the decode branch of the patched attention forward), which appends the
+step's K/V row to every segment and attends in one kernel launch, then
+``decode_all_layers_done`` after the last layer.  The configuration offloads
+nothing (class-B rows are the prefill's survivors), so no step changes the
+layout.  Every layer has its own pool (~2.3 GB in all), far beyond the
+256 MB Infinity Cache.  The step is captured as HIP graphs (two, for the
+alternating offset buffers) and replayed, so the timed region measures the
+GPU, not Python; the eager step is timed as well.
 
 Reported:
-* value          -- whole-step throughput: algorithmic bytes (attention K/V
-                    rows + q/o + appended rows) of the K timed steps / wall time.
-* us_per_layer_step -- decode-attention kernel time per layer-step, from HIP
-                    events around back-to-back attention-only graph replays.
-* roofline       -- the attention kernel: algorithmic bytes per launch /
-                    average launch time vs 8 TB/s.
-* append_us_per_layer_step -- the in-place append kernel alone, per layer-step.
-* compaction     -- the rebuild (compaction + append) kernel on the dense
-                    layout, per layer: class-B segments drop their oldest
-                    window row, every segment gets a new row; µs per layer
-                    and TB/s of rows moved.
-* cpu_baseline   -- the reference's decode layer-step restated in PyTorch
+* value / ms_per_step -- whole decode step through the cache, replayed from
+                    graphs: algorithmic bytes (K/V rows attended + q/o + the
+                    appended rows) of the timed steps / wall time.
+* ms_per_step_eager -- the same step launched from Python.
+* us_per_layer_step -- the fused append + attention launch, per layer-step
+                    (HIP events around graph replays of the 30 launches);
+                    roofline.achieved = its algorithmic bytes / that time.
+* attn_only_us_per_layer_step -- attention without the append, same state.
+* compaction    -- the rebuild (compaction + append, ``rebuild_append_kv``)
+                    kernel on the reference's dense layout, per layer:
+                    class-B segments drop their oldest window row, every
+                    segment gets a new row; µs per layer and TB/s moved.
+* cpu_baseline  -- the reference's decode layer-step restated in PyTorch
                     (torch.cat append + per-segment float32 attention) on the
                     host's cores, on a bounded sample of the same layers.
 
@@ -54,12 +60,14 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4", "cfg5"],
                     help="cfg4 runs whole decode steps through the cache with host->device chunk fetches")
-    ap.add_argument("--kernel", default="auto", choices=["auto", "stream", "mfma", "valu"])
-    ap.add_argument("--attn-reps", type=int, default=20, help="attention-only graph replays for the roofline")
+    ap.add_argument("--attn-reps", type=int, default=20, help="graph replays of the 30 launches for the roofline")
+    ap.add_argument("--score", action="store_true",
+                    help="configure the class-A heads as scored (foldable layers score inside the launch)")
     ap.add_argument("--cpu-sample-layers", type=int, default=0,
                     help="layers timed for the CPU baseline (0 = choose ~15 s of work)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    ap.add_argument("--no-compaction", action="store_true", help="skip the compaction timing")
+    ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy three times (PMC byte calibration)")
     return ap.parse_args()
@@ -81,50 +89,63 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": COPY_CAL_BYTES, "launches": 3}), flush=True)
 
 
-class LayerState:
-    """Slack layout of one layer: each segment owns len + slack rows."""
+def build_cache(cfg, dev, slack_rows: int, score: bool):
+    """A WnWCache holding the workload's state, as a prefill would leave it:
+    every layer's segments of cfg.lengths rows, no host rows, nothing
+    offloaded.  With ``score`` the class-A KV heads' query heads are
+    configured class A (scored every step)."""
+    import numpy as np
+    import torch
 
-    def __init__(self, cfg, layer: int, slack: int, device, gen):
-        import numpy as np
-        import torch
+    from wnw_amd.wnw.cache import WnWCache
+    from wnw_amd.wnw.config import WnWConfig
 
-        self.n = cfg.n_seg
-        d = cfg.head_dim
-        lens = cfg.lengths[layer].astype(np.int64)
-        cap = lens + slack
-        cap = (cap + 7) // 8 * 8
-        base = np.zeros(self.n, np.int64)
-        base[1:] = np.cumsum(cap)[:-1]
-        self.pool_rows = int(cap.sum())
-        self.lens0 = lens
-        self.rows_est = int(lens.sum())  # sizes the grid; the kernel reads the exact rows from cu
-        self.base = torch.from_numpy(base).to(device)
-        self.cap = torch.from_numpy(cap.astype(np.int32)).to(device)
-        cu = np.zeros(self.n + 1, np.int32)
-        cu[1:] = np.cumsum(lens)
-        self.cu = [torch.from_numpy(cu).to(device), torch.zeros(self.n + 1, dtype=torch.int32, device=device)]
-        self.cu_init = torch.from_numpy(cu).to(device)
-        scale_seg = np.tile(cfg.kv_scale[layer], cfg.batch).astype(np.float32)  # segment s = b * Hkv + h
-        row_scale = torch.from_numpy(np.repeat(scale_seg, cap)).to(device).unsqueeze(1)
-        self.k = (torch.randn(self.pool_rows, d, device=device, generator=gen) * row_scale).to(torch.bfloat16)
-        self.v = (torch.randn(self.pool_rows, d, device=device, generator=gen) * row_scale).to(torch.bfloat16)
-        self.q = torch.randn(self.n, cfg.group, d, device=device, generator=gen).to(torch.bfloat16)
-        self.new_k = torch.randn(self.n, d, device=device, generator=gen).to(torch.bfloat16)
-        self.new_v = torch.randn(self.n, d, device=device, generator=gen).to(torch.bfloat16)
-        self.out = torch.empty(self.n, cfg.group, d, dtype=torch.bfloat16, device=device)
+    L, B, Hq, Hkv, D = cfg.layers, cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim
+    G = Hq // Hkv
+    class_a = [l * Hq + kv * G + g for l in range(L) for kv in range(Hkv) if cfg.class_a[l][kv]
+               for g in range(G)] if score else []
+    conf = WnWConfig(chunk_size_s=256, overlap_s=0, token_rate=1.0, class_a=class_a, class_b=[],
+                     retention_ratios=[None] * (L * Hkv), top_k_chunks=0, eviction_lag=2, prefill_score_mode="last",
+                     num_layers=L, num_kv_heads=Hkv, num_q_heads=Hq)
+    cache = WnWCache(conf, L, Hkv, Hq, D, dev, slack_rows=slack_rows)
+    cache.collect_stats(0)  # no memory snapshots: a captured step runs the host side once
+    audio = cfg.audio.astype(np.int64)
+    cache.setup_audio(torch.zeros(B, dtype=torch.int64, device=dev), torch.from_numpy(audio).to(dev), None)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    layer_k, layer_v, seq_lens = [], [], []
+    for l in range(L):
+        lens = cfg.lengths[l].astype(np.int64)
+        scale_seg = np.tile(cfg.kv_scale[l], B).astype(np.float32)  # segment s = b * Hkv + h
+        row_scale = torch.from_numpy(np.repeat(scale_seg, lens)).to(dev).unsqueeze(1)
+        rows = int(lens.sum())
+        layer_k.append((torch.randn(rows, D, device=dev, generator=gen) * row_scale).to(torch.bfloat16))
+        layer_v.append((torch.randn(rows, D, device=dev, generator=gen) * row_scale).to(torch.bfloat16))
+        seq_lens.append([int(x) for x in lens])
+        del row_scale
+    empty = torch.empty(0, D, dtype=torch.bfloat16).pin_memory()
+    cache.load_prefilled_state(layer_k, layer_v, seq_lens, empty, empty, cache.restore_meta,
+                               [set() for _ in range(B)])
+    del layer_k, layer_v
+    torch.cuda.synchronize()
+    return cache
 
-    def reset(self):
-        self.cu[0].copy_(self.cu_init)
 
-    def dense_host(self):
-        """The logical rows of every segment under cu[0], gathered into the
-        reference's dense layout on the host: (k, v, cu)."""
-        import torch
+def step_inputs(cfg, dev, seed: int = 1):
+    """The step's q and new K/V row of every layer (fixed tensors: a captured
+    graph replays the same addresses)."""
+    import torch
 
-        cu = self.cu[0].cpu()
-        lens = (cu[1:] - cu[:-1]).to(torch.int64)
-        idx = torch.cat([self.base[s].cpu() + torch.arange(int(lens[s])) for s in range(self.n)])
-        return self.k.cpu()[idx], self.v.cpu()[idx], cu
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    B, Hq, Hkv, D = cfg.batch, cfg.hq, cfg.hkv, cfg.head_dim
+    out = []
+    for _ in range(cfg.layers):
+        q = torch.randn(B, Hq, 1, D, device=dev, generator=gen).to(torch.bfloat16)
+        k = torch.randn(B, Hkv, 1, D, device=dev, generator=gen).to(torch.bfloat16)
+        v = torch.randn(B, Hkv, 1, D, device=dev, generator=gen).to(torch.bfloat16)
+        out.append((q, k, v))
+    return out
 
 
 def main():
@@ -147,7 +168,7 @@ def main():
 
     from wnw_amd import _lib, workloads
     from wnw_amd.kv import fused_attn
-    from wnw_amd.kv.kernels import append_inplace
+    from wnw_amd.wnw.session import decode_attention
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -155,207 +176,189 @@ def main():
     _lib.ensure_init(dev)
     cfg = workloads.CONFIGS[args.config]()
     L, N, G, D = cfg.layers, cfg.n_seg, cfg.group, cfg.head_dim
-    total_steps = args.warmup + args.steps
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(0)
-    print(f"# config {cfg.name}: layers={L} n_seg={N} G={G} D={D} steps={args.steps} warmup={args.warmup}",
-          flush=True)
-    # slack: one row per step, plus the four appends of the append-only timing
-    layers = [LayerState(cfg, l, total_steps + 6, dev, gen) for l in range(L)]
-    torch.cuda.synchronize()
-    ws = fused_attn.AttnWorkspace(dev)
-    ws.get(N, G, D)
+    graph = not args.no_graph
+    warm_even = args.warmup + args.warmup % 2
+    steps_even = args.steps + args.steps % 2
+    # appends of the run: the eager steps, and with graphs two captured steps,
+    # their replays, two captured sets of fused launches and their replays;
+    # the slack covers them all, so no pool is rebuilt on the way
+    appends = args.warmup + args.steps
+    if graph:
+        appends += 2 + 2 + warm_even + steps_even + 2 + 2 + 2 * args.attn_reps
+    cache = build_cache(cfg, dev, slack_rows=appends + 16, score=args.score)
+    inputs = step_inputs(cfg, dev)
     scale = D ** -0.5
+    print(f"# config {cfg.name}: layers={L} n_seg={N} G={G} D={D} steps={args.steps} warmup={args.warmup} "
+          f"score={args.score}", flush=True)
 
-    def step_launches(parity: int):
-        for st in layers:
-            cu_old, cu_new = st.cu[parity], st.cu[1 - parity]
-            append_inplace(st.k, st.v, st.new_k, st.new_v, cu_old, cu_new, st.base, st.cap)
-            fused_attn.decode_attn(st.q, st.k, st.v, cu_new, scale, seg_base=st.base, total_rows=st.rows_est,
-                                   out=st.out, workspace=ws, kernel=args.kernel)
+    def step():
+        for l, (q, k, v) in enumerate(inputs):
+            decode_attention(cache, l, q, k, v, scale, fused=True)
 
-    def append_launches(parity: int):
-        for st in layers:
-            append_inplace(st.k, st.v, st.new_k, st.new_v, st.cu[parity], st.cu[1 - parity], st.base, st.cap)
+    def launch_bytes(rows_before: int) -> int:
+        """Algorithmic bytes of one fused launch: K/V of every row after the
+        append, q in, o out, and the appended rows (read and written)."""
+        return (rows_before + N) * D * 2 * 2 + 2 * N * G * D * 2 + N * D * 2 * 2 * 2
 
-    def attn_launches():
-        for st in layers:
-            fused_attn.decode_attn(st.q, st.k, st.v, st.cu[0], scale, seg_base=st.base, total_rows=st.rows_est,
-                                   out=st.out, workspace=ws, kernel=args.kernel)
+    def steps_bytes(rows_before: list[int], n: int) -> int:
+        return sum(launch_bytes(r + i * N) for i in range(n) for r in rows_before)
 
-    stream = torch.cuda.Stream(device=dev)
-    graphs = None
-    attn_graph = None
-    append_graphs = None
-    if not args.no_graph:
-        # capture on a side stream (default priority), then replay
-        with torch.cuda.stream(stream):
-            ws.get(N, G, D)
-        torch.cuda.synchronize()
-        graphs = []
-        for parity in (0, 1):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                step_launches(parity)
-            graphs.append(g)
-        attn_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(attn_graph, stream=stream):
-            attn_launches()
-        append_graphs = []
-        for parity in (0, 1):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                append_launches(parity)
-            append_graphs.append(g)
-        torch.cuda.synchronize()
-        for st in layers:  # capture does not execute; start from the initial offsets
-            st.reset()
-        torch.cuda.synchronize()
-
-    def run_step(t: int):
-        if graphs is not None:
-            graphs[t % 2].replay()
-        else:
-            step_launches(t % 2)
-
-    # ---- warmup + timed decode steps --------------------------------------
-    ctx = torch.cuda.stream(stream) if graphs is not None else torch.cuda.stream(torch.cuda.current_stream())
-    with ctx:
-        for t in range(args.warmup):
-            run_step(t)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for t in range(args.warmup, total_steps):
-            run_step(t)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    assert _lib.device_error() == 0, "device error during the timed steps"
-    step_s = (t1 - t0) / args.steps
-
-    # bytes of the timed steps: rows attended at step t are lens0 + t + 1 per segment
-    attn_bytes_total = 0
-    append_bytes_total = 0
-    for t in range(args.warmup, total_steps):
-        for st in layers:
-            rows = int(st.lens0.sum()) + N * (t + 1)
-            attn_bytes_total += rows * D * 2 * 2 + 2 * N * G * D * 2
-            append_bytes_total += 2 * N * D * 2 * 2  # read new row + write it, K and V
-    value_tbs = (attn_bytes_total + append_bytes_total) / (t1 - t0) / 1e12
-
-    # ---- attention-only kernel timing (state after the timed steps) -------
-    # cu[0] now holds the offsets after an even number of steps, or cu[1]:
-    final_parity = total_steps % 2
-    for st in layers:
-        if final_parity == 1:
-            st.cu[0].copy_(st.cu[1])
+    # ---- eager steps (Python per layer) -----------------------------------
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
-    rows_attn = [int(st.cu[0][-1].item()) for st in layers]
-    bytes_per_launch = [r * D * 2 * 2 + 2 * N * G * D * 2 for r in rows_attn]
-    with torch.cuda.stream(stream):
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        if attn_graph is not None:
-            attn_graph.replay()
-        else:
-            attn_launches()
-        ev0.record(stream)
-        for _ in range(args.attn_reps):
-            if attn_graph is not None:
-                attn_graph.replay()
-            else:
+    rows_eager = list(cache._rows)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_s = (time.perf_counter() - t0) / args.steps
+    assert _lib.device_error() == 0, "device error during the eager steps"
+    value = steps_bytes(rows_eager, args.steps) / (eager_s * args.steps) / 1e12
+
+    fused_us = attn_us = step_s = achieved = attn_gbs = fused_bytes = None
+    rows_attn = list(cache._rows)
+    if graph:
+        stream = torch.cuda.Stream(device=dev)  # default priority
+        with torch.cuda.stream(stream):  # workspaces of the capture stream, made before capture
+            fused_attn.workspace_for(dev).get(N, G, D)
+            if args.score:
+                fused_attn.workspace_for(dev).get(N, G, D, score=True, max_audio=cache._max_audio)
+        torch.cuda.synchronize()
+        rows_dev = list(cache._rows)  # the device state before any capture
+        # whole decode steps through the cache: two captures (alternating offsets)
+        step_graphs = []
+        for _ in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+            step_graphs.append(g)
+        # the fused launches alone (no end-of-step hook)
+        fused_graphs = []
+        for _ in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for l, (q, k, v) in enumerate(inputs):
+                    q_flat = q.squeeze(2).reshape(N, G, D)
+                    cache.decode_step_attention(l, q_flat, q, k, v, scale, True)
+            fused_graphs.append(g)
+        # the captures ran the host side of 4 steps, the device none: the
+        # host mirrors are 4 steps ahead until 4 replays have run
+
+        def replay(graphs, n):
+            for i in range(n):
+                graphs[i % 2].replay()
+
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            replay(step_graphs, 2 + warm_even)
+            stream.synchronize()
+            done = 2 + warm_even
+            t0 = time.perf_counter()
+            replay(step_graphs, steps_even)
+            stream.synchronize()
+            step_s = (time.perf_counter() - t0) / steps_even
+            bytes_timed = steps_bytes([r + done * N for r in rows_dev], steps_even)
+            done += steps_even
+            # the fused launches: HIP events on the replay stream
+            replay(fused_graphs, 2)
+            done += 2
+            rows_fused = [r + done * N for r in rows_dev]
+            e0.record(stream)
+            replay(fused_graphs, 2 * args.attn_reps)
+            e1.record(stream)
+            e1.synchronize()
+            done += 2 * args.attn_reps
+        fused_us = e0.elapsed_time(e1) * 1e3 / (2 * args.attn_reps * L)
+        cache.advance_replayed_steps(done - 4)
+        assert _lib.device_error() == 0, "device error during the graph replays"
+        assert list(cache._rows) == [r + done * N for r in rows_dev]
+        value = bytes_timed / (step_s * steps_even) / 1e12
+        # average over the timed launches: rows grow by N per launch
+        fused_bytes = float(np.mean([launch_bytes(r + i * N) for r in rows_fused
+                                     for i in range(2 * args.attn_reps)]))
+        achieved = fused_bytes / (fused_us * 1e-6) / 1e9
+        # attention alone (no append) on the final state
+        rows_attn = list(cache._rows)
+        outs = [torch.empty(N, G, D, dtype=torch.bfloat16, device=dev) for _ in range(L)]
+
+        def attn_launches():
+            for l, (q, _, _) in enumerate(inputs):
+                q_flat = q.squeeze(2).reshape(N, G, D)
+                fused_attn.decode_attn(q_flat, cache.layer_k[l], cache.layer_v[l], cache.cu_seqlens_k[l], scale,
+                                       seg_base=cache.seg_base[l], total_rows=cache._rows[l], out=outs[l])
+
+        with torch.cuda.stream(stream):
+            ga = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(ga, stream=stream):
                 attn_launches()
-        ev1.record(stream)
-        ev1.synchronize()
-    attn_ms = ev0.elapsed_time(ev1)
-    launches = args.attn_reps * L
-    us_per_launch = attn_ms * 1e3 / launches
-    avg_bytes = float(np.mean(bytes_per_launch))
-    achieved_gbs = avg_bytes / (us_per_launch * 1e-6) / 1e9
-    assert _lib.device_error() == 0, "device error during attention timing"
+            ga.replay()
+            e0.record(stream)
+            for _ in range(args.attn_reps):
+                ga.replay()
+            e1.record(stream)
+            e1.synchronize()
+        attn_us = e0.elapsed_time(e1) * 1e3 / (args.attn_reps * L)
+        assert _lib.device_error() == 0, "device error during attention timing"
+        attn_bytes = float(np.mean([r * D * 2 * 2 + 2 * N * G * D * 2 for r in rows_attn]))
+        attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
 
-    # ---- append-only kernel timing: two appends (there and back) per rep --
-    # The slack leaves room for them: rows stay within each segment's capacity.
-    app_reps = 2
-    with torch.cuda.stream(stream):
-        ev2 = torch.cuda.Event(enable_timing=True)
-        ev3 = torch.cuda.Event(enable_timing=True)
-        ev2.record(stream)
-        for r in range(app_reps):
-            for parity in (0, 1):
-                if append_graphs is not None:
-                    append_graphs[parity].replay()
-                else:
-                    append_launches(parity)
-        ev3.record(stream)
-        ev3.synchronize()
-    append_us = ev2.elapsed_time(ev3) * 1e3 / (2 * app_reps * L)
-    assert _lib.device_error() == 0, "device error during append timing"
-
-    # ---- compaction timing: one rebuild (a4) per layer ---------------------
-    compact = compaction_timing(cfg, layers, dev, stream, graphs is not None)
-    assert _lib.device_error() == 0, "device error during compaction timing"
-
-    # ---- CPU baseline: float64 C oracle on a bounded sample ---------------
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(cfg, layers, scale, args.cpu_sample_layers)
-
+    compact = None if args.no_compaction else compaction_timing(cfg, cache, inputs, dev)
+    cpu = None if args.no_cpu else cpu_baseline(cfg, cache, inputs, scale, args.cpu_sample_layers)
     line = {
-        "metric": METRIC,
-        "value": round(value_tbs, 4),
-        "unit": "TB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
+        "metric": METRIC, "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(step_s * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
+        "ms_per_step": round((step_s if step_s is not None else eager_s) * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": cfg.name, "layers": L, "batch": cfg.batch, "hq": cfg.hq, "hkv": cfg.hkv,
                    "head_dim": D, "n_seg": N, "rows_per_layer_step": int(np.mean(rows_attn)),
-                   "kernel": args.kernel, "graph": graphs is not None, "notes": cfg.notes},
-        "us_per_layer_step": round(us_per_launch, 3),
-        "append_us_per_layer_step": round(append_us, 3),
+                   "path": "WnWCache (slack layout) + session.decode_attention: fused append + attention",
+                   "graph": graph, "score": args.score, "notes": cfg.notes},
+        "ms_per_step_eager": round(eager_s * 1e3, 4),
+        "us_per_layer_step": None if fused_us is None else round(fused_us, 3),
+        "attn_only_us_per_layer_step": None if attn_us is None else round(attn_us, 3),
+        "attn_only_TBs": None if attn_gbs is None else round(attn_gbs / 1e3, 4),
         "compaction": compact,
-        "attn_TBs": round(achieved_gbs / 1e3, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name)},
+        "roofline": None if achieved is None else {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name),
+            "kernel": "attn_stream_kernel, fused append + attention", "bytes_per_launch": int(fused_bytes),
+            "traffic_source": f"rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated "
+                              f"(profiles/decode_attn_{cfg.name}_traffic.json)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
 
-def compaction_timing(cfg, layers, dev, stream, use_graph: bool, reps: int = 5) -> dict:
-    """One ``rebuild_append_kv`` per layer on the dense layout (the reference's
-    layout): every class-B segment drops row 4 (sink + window: the oldest
-    window row, one relative evict range [4, 5)), every segment gets the
-    step's new row, nothing is loaded.  Bytes = rows moved: the kept and new
-    rows read, every output row written, K and V."""
+def compaction_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
+    """One ``rebuild_append_kv`` per layer on the reference's dense layout
+    (the cache's rows gathered densely): every class-B segment drops row 4
+    (sink + window: the oldest window row, one relative evict range [4, 5)),
+    every segment gets the step's new row, nothing is loaded.  Bytes = rows
+    moved: the kept and new rows read, every output row written, K and V."""
     import numpy as np
     import torch
 
     from wnw_amd.wnw.kernels import rebuild_append_kv
 
-    D = cfg.head_dim
+    D, N = cfg.head_dim, cfg.n_seg
     i32 = dict(dtype=torch.int32, device=dev)
     calls, moved = [], 0
-    for li, st in enumerate(layers):
-        lens = st.lens0.astype(np.int64)
-        base = st.base.cpu().numpy()
-        idx = torch.from_numpy(np.concatenate([b + np.arange(n) for b, n in zip(base, lens)])).to(dev)
-        dk, dv = st.k.index_select(0, idx), st.v.index_select(0, idx)
+    for li in range(cfg.layers):
+        dk, dv = cache.dense_kv(li)
+        lens = np.asarray(cache.seq_lens[li], np.int64)
         class_b = ~np.tile(cfg.class_a[li].astype(bool), cfg.batch)
-        n_ev = class_b.astype(np.int64)
+        n_ev = (class_b & (lens > 4)).astype(np.int64)
         old_cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
         new_lens = lens - n_ev + 1
         new_cu = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
         ev_off = np.concatenate([[0], np.cumsum(n_ev)]).astype(np.int32)
         n_b = int(n_ev.sum())
-        args = (dk, dv, st.new_k, st.new_v, dk[:0], dv[:0], torch.from_numpy(old_cu).to(dev),
-                torch.from_numpy(new_cu).to(dev), torch.full((st.n,), -1, **i32), torch.zeros(st.n, **i32),
-                torch.from_numpy(ev_off).to(dev), torch.full((n_b,), 4, **i32), torch.full((n_b,), 5, **i32), 1)
+        nk = inputs[li][1].reshape(N, D)
+        nv = inputs[li][2].reshape(N, D)
+        args = (dk, dv, nk, nv, dk[:0], dv[:0], torch.from_numpy(old_cu).to(dev), torch.from_numpy(new_cu).to(dev),
+                torch.full((N,), -1, **i32), torch.zeros(N, **i32), torch.from_numpy(ev_off).to(dev),
+                torch.full((n_b,), 4, **i32), torch.full((n_b,), 5, **i32), 1)
         calls.append((args, int(new_cu[-1])))
         moved += int(new_cu[-1]) * D * 2 * 2 * 2
     torch.cuda.synchronize()
@@ -364,23 +367,22 @@ def compaction_timing(cfg, layers, dev, stream, use_graph: bool, reps: int = 5) 
         for args, tot in calls:
             rebuild_append_kv(*args, total_out=tot)
 
+    stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
         launches()  # allocates the outputs before capture
-        graph = None
-        if use_graph:
-            torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                launches()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            launches()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        (graph.replay if graph is not None else launches)()
+        graph.replay()
         e0.record(stream)
         for _ in range(reps):
-            (graph.replay if graph is not None else launches)()
+            graph.replay()
         e1.record(stream)
         e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
-    bytes_per_launch = moved / len(layers)
+    us = e0.elapsed_time(e1) * 1e3 / (reps * cfg.layers)
+    bytes_per_launch = moved / cfg.layers
     return {"kernel": "rebuild_append_kernel", "us_per_layer_step": round(us, 3),
             "bytes_per_launch": int(bytes_per_launch),
             "TBs": round(bytes_per_launch / (us * 1e-6) / 1e12, 3),
@@ -389,7 +391,9 @@ def compaction_timing(cfg, layers, dev, stream, use_graph: bool, reps: int = 5) 
 
 
 def traffic_from_profiles(workload: str):
-    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if present."""
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if
+    present."""
     path = os.path.join(ROOT, "profiles", f"decode_attn_{workload}_traffic.json")
     if not os.path.exists(path):
         return None
@@ -415,13 +419,12 @@ def cpu_threads() -> int:
     return max(1, n)
 
 
-def cpu_baseline(cfg, layers, scale, sample_layers: int, budget_s: float = 15.0):
+def cpu_baseline(cfg, cache, inputs, scale, sample_layers: int, budget_s: float = 15.0):
     """The reference's decode layer-step in PyTorch on the host's cores
     (``oracle/torch_cpu.py``): the append of the step's row to every segment
     (``torch.cat``, out of place) and per-segment float32 attention, on a
-    bounded sample of the workload's layers (the dense logical rows of each
-    layer, copied to the host before timing)."""
-    import numpy as np
+    bounded sample of the workload's layers (the cache's rows in the dense
+    layout, copied to the host before timing)."""
     import torch
 
     from oracle import torch_cpu
@@ -429,14 +432,17 @@ def cpu_baseline(cfg, layers, scale, sample_layers: int, budget_s: float = 15.0)
     threads = cpu_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
-    D, G = cfg.head_dim, cfg.group
+    D, G, N = cfg.head_dim, cfg.group, cfg.n_seg
     elapsed, done, bytes_done = 0.0, 0, 0
-    limit = sample_layers if sample_layers > 0 else len(layers)
+    limit = sample_layers if sample_layers > 0 else cfg.layers
     try:
-        for li, st in enumerate(layers[:limit]):
-            k, v, cu = st.dense_host()
-            nk, nv, q = st.new_k.cpu(), st.new_v.cpu(), st.q.cpu()
-            cu_old = cu.tolist()
+        for li in range(limit):
+            dk, dv = cache.dense_kv(li)
+            k, v = dk.cpu(), dv.cpu()
+            cu_old = cache.cu_list(li)
+            q, nk, nv = (t.cpu() for t in inputs[li])
+            q = q.reshape(N, G, D)
+            nk, nv = nk.reshape(N, D), nv.reshape(N, D)
             cu_new = [c + i for i, c in enumerate(cu_old)]
             t0 = time.perf_counter()
             k2 = torch_cpu.append_by_cat(k, nk, cu_old)
@@ -444,7 +450,7 @@ def cpu_baseline(cfg, layers, scale, sample_layers: int, budget_s: float = 15.0)
             torch_cpu.decode_attn(q, k2, v2, cu_new, scale)
             elapsed += time.perf_counter() - t0
             done += 1
-            bytes_done += cu_new[-1] * D * 2 * 2 + 2 * cfg.n_seg * G * D * 2
+            bytes_done += cu_new[-1] * D * 2 * 2 + 2 * N * G * D * 2
             if sample_layers <= 0 and elapsed > budget_s:
                 break
     finally:

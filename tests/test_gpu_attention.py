@@ -502,3 +502,12 @@ def test_total_rows_only_sizes_the_grid(gpu, n_seg):
         assert _lib.device_error() == 0
         ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
         assert ok, f"total_rows={total}: {msg}"
+
+
+def test_fused_append_many_tiny_segments(gpu):
+    """Segments of 1-3 rows after the append: each wave ends many segments,
+    more than it can save for the end of its stream, so the surplus new
+    rows are stored during the stream."""
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(0, 3, 2000)]
+    _check_append(_append_case(gpu, lens, 4, 128, "bfloat16", seed=77), "bfloat16")

@@ -93,30 +93,41 @@ def _prefill(cache, dev, gen):
     cache.prefill_all_layers_done()
 
 
+# layouts: the default slack layout (plans relocate changed segments into
+# the pool's tail), 3 rows of slack and no tail (a relayout every few
+# appends, and every plan rebuilds the whole layer), and the reference's
+# dense layout
+LAYOUTS = {"slack": dict(slack_rows=256), "tight": dict(slack_rows=3, tail=0), "dense": dict(slack_rows=0)}
+
+
+@pytest.mark.parametrize("layout", ["slack", "tight", "dense"])
 @pytest.mark.parametrize("variant,fused,host_gather", [("wnw", True, False), ("wnw", False, False),
                                                        ("wnw_fallback", True, False), ("wnw_cpp", True, False),
                                                        ("wnw", True, True), ("wnw_cpp", True, True)])
-def test_decode_steps_match_simulation(variant, fused, host_gather, monkeypatch):
+def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monkeypatch):
     dev = torch.device("cuda", 0)
     if host_gather:  # loads through the host gather + staging copy instead of the device gather
         monkeypatch.setenv("WNW_HOST_GATHER", "1")
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     cls = _recording(WnWCppCache if variant == "wnw_cpp" else WnWCache)
-    cache = cls(_config(), L, H, HQ, D, dev)
+    lay = LAYOUTS[layout]
+    cache = cls(_config(), L, H, HQ, D, dev, slack_rows=lay["slack_rows"])
+    if "tail" in lay:
+        cache.tail_rows_min = cache.tail_factor = lay["tail"]
     cache.rec_acc, cache.rec_topk = [], []
     if variant == "wnw_fallback":
         cache.use_triton_rebuild = False
     cache.collect_stats(1)  # a snapshot every decode step
-    print(f"cache variant={variant} fused={fused} host_gather={host_gather}", flush=True)
+    print(f"cache variant={variant} fused={fused} host_gather={host_gather} layout={layout}", flush=True)
     _prefill(cache, dev, gen)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
     assert cache._device_gather == (not host_gather)
 
     # simulation state, taken from the prefilled cache
-    K = [_bits(cache.layer_k[l]) for l in range(L)]
-    V = [_bits(cache.layer_v[l]) for l in range(L)]
+    K = [_bits(cache.dense_kv(l)[0]) for l in range(L)]
+    V = [_bits(cache.dense_kv(l)[1]) for l in range(L)]
     lens = [list(cache.seq_lens[l]) for l in range(L)]
     host_k, host_v = _bits(cache.cpu_restore_k), _bits(cache.cpu_restore_v)
     meta = [[[[None if m is None else op.SegMeta(m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
@@ -177,8 +188,9 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, monkeypatch)
                 K[l] = oracle.interleave_append(K[l], nk, cu_old, cu_new, dtype=oracle.DT_BF16)
                 V[l] = oracle.interleave_append(V[l], nv, cu_old, cu_new, dtype=oracle.DT_BF16)
                 lens[l] = [x + 1 for x in lens[l]]
-            np.testing.assert_array_equal(_bits(cache.layer_k[l]), K[l], err_msg=f"K step {t} layer {l}")
-            np.testing.assert_array_equal(_bits(cache.layer_v[l]), V[l], err_msg=f"V step {t} layer {l}")
+            dk, dv = cache.dense_kv(l)
+            np.testing.assert_array_equal(_bits(dk), K[l], err_msg=f"K step {t} layer {l}")
+            np.testing.assert_array_equal(_bits(dv), V[l], err_msg=f"V step {t} layer {l}")
             cu = np.array(op.cu_from_lens(lens[l]), np.int32)
             np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu)
             q_flat = _bits(qs[l].reshape(B * H, G, D))
@@ -224,4 +236,58 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, monkeypatch)
     for b in range(B):
         assert set(cache._planner.get_loaded_segments(b)) == o.loaded[b]
     assert n_plans > 0, "no compaction happened: the test would be vacuous"
+    counts = cache.layout_counts
+    if layout == "slack":  # plans relocate changed segments until the tail is used up
+        assert counts["relocate"] > 0 and counts["relayout"] == L, counts
+    elif layout == "tight":  # no tail: every plan rebuilds whole layers
+        assert counts["relocate"] == 0 and counts["relayout_plan"] > 0, counts
+    else:
+        assert counts == {"relayout": 0, "relayout_plan": 0, "relocate": 0}, counts
     assert any(want_events), "no decode-time load happened: the stats check would be vacuous"
+
+
+def test_appends_beyond_the_slack_rebuild_the_pool():
+    """Slack of one row and no plans (nothing offloaded): appends run out of
+    room every few steps and the layer moves to a fresh pool; its logical
+    rows and offsets stay those of the reference's appends (bit-exact), and
+    attention over them matches the oracle."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(12)
+    Hq, Hkv, Bn, Ln = 8, 2, 3, 2
+    conf = WnWConfig(chunk_size_s=8, overlap_s=0, token_rate=1.0, class_a=[], class_b=[],
+                     retention_ratios=[None] * (Ln * Hkv), top_k_chunks=0, eviction_lag=2,
+                     prefill_score_mode="last", num_layers=Ln, num_kv_heads=Hkv, num_q_heads=Hq)
+    cache = WnWCache(conf, Ln, Hkv, Hq, D, dev, slack_rows=1)
+    cache.collect_stats(0)
+    cache.setup_audio(torch.zeros(Bn, dtype=torch.int64, device=dev), torch.full((Bn,), 16, device=dev), None)
+    N = Bn * Hkv
+    lens = [[int(x) for x in rng.integers(0, 40, N)] for _ in range(Ln)]
+    K = [oracle.f32_to_bf16_bits(rng.standard_normal((sum(x), D)).astype(np.float32)) for x in lens]
+    V = [oracle.f32_to_bf16_bits(rng.standard_normal((sum(x), D)).astype(np.float32)) for x in lens]
+    tb = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)  # noqa: E731
+    empty = torch.empty(0, D, dtype=torch.bfloat16).pin_memory()
+    cache.load_prefilled_state([tb(k) for k in K], [tb(v) for v in V], lens, empty, empty, cache.restore_meta,
+                               [set() for _ in range(Bn)])
+    scale = D ** -0.5
+    for t in range(20):
+        for l in range(Ln):
+            q = oracle.f32_to_bf16_bits(rng.standard_normal((Bn, Hq, 1, D)).astype(np.float32))
+            nk = oracle.f32_to_bf16_bits(rng.standard_normal((Bn, Hkv, 1, D)).astype(np.float32))
+            nv = oracle.f32_to_bf16_bits(rng.standard_normal((Bn, Hkv, 1, D)).astype(np.float32))
+            out = decode_attention(cache, l, tb(q), tb(nk), tb(nv), scale, fused=True)
+            cu_old = np.array(op.cu_from_lens(lens[l]), np.int32)
+            cu_new = cu_old + np.arange(N + 1, dtype=np.int32)
+            K[l] = oracle.interleave_append(K[l], nk.reshape(N, D), cu_old, cu_new, dtype=oracle.DT_BF16)
+            V[l] = oracle.interleave_append(V[l], nv.reshape(N, D), cu_old, cu_new, dtype=oracle.DT_BF16)
+            lens[l] = [x + 1 for x in lens[l]]
+            torch.cuda.synchronize()
+            assert _lib.device_error() == 0, f"step {t} layer {l}"
+            dk, dv = cache.dense_kv(l)
+            np.testing.assert_array_equal(_bits(dk), K[l], err_msg=f"K step {t} layer {l}")
+            np.testing.assert_array_equal(_bits(dv), V[l], err_msg=f"V step {t} layer {l}")
+            np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu_new)
+            ref = oracle.decode_attn(q.reshape(N, Hq // Hkv, D), K[l], V[l], cu_new, scale, dtype=oracle.DT_BF16)
+            got = oracle.to_f64(_bits(out.reshape(N, Hq // Hkv, D)), oracle.DT_BF16)
+            ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+            assert ok, f"attention step {t} layer {l}: {msg}"
+    assert cache.layout_counts["relayout"] > 2 * Ln, cache.layout_counts

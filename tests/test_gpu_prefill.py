@@ -71,8 +71,9 @@ def test_prefill_matches_restatement(gpu, global_topk):
     pf.all_layers_done((D,), np.uint16)
     assert _lib.device_error() == 0
     for l in range(L):
-        np.testing.assert_array_equal(_bits(cache.layer_k[l]), pf.layer_k[l], err_msg=f"K layer {l}")
-        np.testing.assert_array_equal(_bits(cache.layer_v[l]), pf.layer_v[l], err_msg=f"V layer {l}")
+        dk, dv = cache.dense_kv(l)  # the logical rows, whatever the physical layout
+        np.testing.assert_array_equal(_bits(dk), pf.layer_k[l], err_msg=f"K layer {l}")
+        np.testing.assert_array_equal(_bits(dv), pf.layer_v[l], err_msg=f"V layer {l}")
         assert list(cache.seq_lens[l]) == list(pf.seq_lens[l])
         cu = np.concatenate([[0], np.cumsum(pf.seq_lens[l])]).astype(np.int32)
         np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu)

@@ -20,11 +20,15 @@
 // the segment's arrival counter; the last arriver merges the partials by
 // log-sum-exp and writes the output (no second kernel launch).
 //
-// Fused append (streaming kernel, APPEND): every segment first gains the
-// step's new row, new_k/new_v[s], at physical row base[s] + len_old[s]
-// (len_old from cu); the step that covers that row reads it from new_k/new_v
-// instead of the pool, and the wave that processed it writes it into the
-// pool from LDS.  cu_out = cu + arange(n_seg + 1) is written by workgroup 0.
+// Fused append (streaming kernel, APPEND): every segment gains the step's
+// new row, new_k/new_v[s], at physical row base[s] + len_old[s] (len_old from
+// cu).  The split and the stream cover the old rows only, exactly as without
+// the append; the first step of every piece also copies its segment's new
+// row into LDS beside q, and the wave that finishes a segment folds that row
+// into its softmax state (one more logit and one more V row) before the
+// state is written or merged.  The new rows are stored into the pools, and
+// cu_out = cu + arange(n_seg + 1) written, at the end of the kernel, where
+// no wait of the stream waits for their acknowledgement.
 //
 // Three kernels implement this split.  The streaming kernel (bf16/f16, D 64 or
 // 128, G <= 8; the default there) gives each wave a quarter of its
@@ -95,7 +99,7 @@ __device__ __forceinline__ bool seg_valid(int64_t lo, int64_t len, int64_t b, in
 
 // Per-workgroup schedule, shared through LDS.
 struct SchedLds {
-  int64_t R;       // logical rows partitioned: cu[n_seg] (+ n_seg with APPEND)
+  int64_t R;       // logical rows partitioned: cu[n_seg]
   int64_t KV;      // physical rows (bounds)
   int64_t B0, B1;  // this workgroup's logical row range
   int32_t P;       // effective number of workgroups (<= R)
@@ -153,12 +157,42 @@ __device__ __forceinline__ void wg_range(int64_t R, int64_t P, uint64_t inv, int
   B1 = split_start((pid + 1) * kSplitWaves, R, P, inv);
 }
 
+// APPEND, a segment with no old rows: its only row is the new one, so every
+// head's output is that V row (softmax weight 1) and its statistics are
+// (logit, 1).  One thread does it all; rare, since a decode-time segment
+// holds its earlier steps' rows.  With store_row the row also goes into the
+// pools at physical row b.
+template <typename T>
+__device__ __forceinline__ void append_only_segment(const AttnParams& p, int D, int s, int64_t b, bool store_row) {
+  const int G = p.G;
+  const T* nk = (const T*)p.new_k + (int64_t)s * D;
+  const T* nv = (const T*)p.new_v + (int64_t)s * D;
+  const T* q = (const T*)p.q + (int64_t)s * G * D;
+  for (int g = 0; g < G; ++g) {
+    float dot = 0.f;
+    for (int e = 0; e < D; ++e) dot += Elem<T>::to_f32(q, g * D + e) * Elem<T>::to_f32(nk, e);
+    for (int e = 0; e < D; ++e) store_elem<T>(p.out, ((int64_t)s * G + g) * D + e, Elem<T>::to_f32(nv, e));
+    if (p.lse) {
+      gptr_w<float>(p.lse)[((int64_t)s * G + g) * 2] = dot * p.scale_log2;
+      gptr_w<float>(p.lse)[((int64_t)s * G + g) * 2 + 1] = 1.f;
+    }
+  }
+  if (store_row) {
+    WNW_GLOBAL uint16_t* kd = gptr_w<uint16_t>(const_cast<void*>(p.k)) + b * D;
+    WNW_GLOBAL uint16_t* vd = gptr_w<uint16_t>(const_cast<void*>(p.v)) + b * D;
+    for (int e = 0; e < D; ++e) {
+      kd[e] = ((const uint16_t*)nk)[e];
+      vd[e] = ((const uint16_t*)nv)[e];
+    }
+  }
+}
+
 // Workgroup prologue: one pass over cu / base (all threads, independent
 // loads) finds the segments whose logical rows overlap this workgroup's
 // range, checks the table, and writes the outputs of empty segments (zeros)
 // and of invalid ones (NaN) owned by this workgroup (segment i -> workgroup
-// i % grid).  With APPEND, lengths include the new row and workgroup 0
-// writes cu_out.
+// i % grid).  With APPEND, an empty segment's output is its new row (the
+// owner stores that row into the pool too) and workgroup 0 writes cu_out.
 template <typename T, int NT, bool XL = false, bool APPEND = false>
 __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& sl) {
   const int tid = threadIdx.x;
@@ -214,7 +248,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
   const int32_t cu_end = cu[N];
   load_chunk(0);
   __syncthreads();
-  const int64_t R = max((int64_t)0, (int64_t)cu_end + (APPEND ? N : 0));
+  const int64_t R = max((int64_t)0, (int64_t)cu_end);
   const int64_t P = effective_wgs(R);
   const bool active = pid < P;
   int64_t B0, B1;
@@ -232,17 +266,22 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       }
       int64_t len = (int64_t)hi[u] - lo[u];
       const int64_t b = p.base ? bs[u] : (int64_t)lo[u];
+      bool neg = false;
       if (len < 0) {  // corrupt offsets: treated as an empty segment
         raise_device_error(p.err, WNW_DEVERR_ORDER);
         sl.order_bad = 1;
         len = 0;
-      } else if (APPEND) {
-        ++len;
-        if (len > cp[u]) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
+        neg = true;
+      } else if (APPEND && len + 1 > cp[u]) {
+        raise_device_error(p.err, WNW_DEVERR_CAPACITY);
       }
       const bool owner = (i % (int)gridDim.x) == (int)pid;
       if (!seg_valid(lo[u], len, b, R, KV)) {
         if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+        if (APPEND && len == 0 && !neg) {  // only the new row: it is the output
+          if (owner) append_only_segment<T>(p, D, i, b, len + 1 <= cp[u] && b >= 0 && b < KV);
+          continue;
+        }
         if (owner) {
           const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
           for (int e = 0; e < p.G * D; ++e) store_elem<T>(p.out, (int64_t)i * p.G * D + e, fill);
@@ -925,10 +964,22 @@ struct StreamGeom {
   static constexpr int kSlot = 2 * kMaxGroupS * 4 + kMaxGroupS * DP * 4;  // merge slot bytes
 };
 
+// Fused append: new rows a wave keeps (K and V, plus the physical row) to
+// store at the end of the kernel; beyond that they are stored at once.
+static constexpr int kSaveRows = 4;
+
+// q slot bytes: q's G rows, rounded to 256; with the fused append 1 KB more
+// for the segment's new K and V rows (one 64-lane load).
+__host__ __device__ constexpr int stream_qslot(int G, int D, bool append) {
+  return ((G * D * 2 + 255) & ~255) + (append ? 1024 : 0);
+}
+
 // LDS bytes of the streaming kernel: per wave two (K, V) step buffers and two
-// q slots of qslot bytes; the merge slots reuse the step buffers.
-__host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot) {
-  return NW * (4 * kSRows * D * 2 + 2 * qslot);
+// q slots of qslot bytes, and with the fused append the kept new rows
+// (kSaveRows x (K + V rows + 8-byte row index)); the merge slots reuse the
+// step buffers.
+__host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot, bool append = false) {
+  return NW * (4 * kSRows * D * 2 + 2 * qslot + (append ? kSaveRows * (2 * D * 2 + 8) : 0));
 }
 
 // One step of a wave's stream: rows [row0, row0 + nrows) of segment s.
@@ -938,7 +989,8 @@ struct SStep {
   int32_t s, nrows, seg_len, qslot;
   int32_t first, last, whole;
   int32_t t0, alen;  // audio index of the first row; audio rows whose logits are kept (0: none)
-  int32_t newrow;    // APPEND: 1 = the step's last row is the segment's new row, 2 = and it is written to the pool
+  int32_t ends_seg;  // APPEND: the step ends its segment (its new row is folded in after it)
+  int32_t wr;        // APPEND: the segment's lane in the walk's window (its capacity)
 };
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
@@ -964,7 +1016,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   using Ops = StreamOps<T>;
   constexpr int NT = NW * 64;
   constexpr int RB = G_::RB, SB = G_::SB, NI = G_::NI, RPI = G_::RPI, CH = G_::CH, NC = G_::NC, NTD = G_::NTD;
-  constexpr int E = NI + QD + NI;  // loads per step
+  constexpr int QX = QD + (APPEND ? 1 : 0);  // first-step loads besides K and V: q (and the new row)
+  constexpr int E = NI + QX + NI;  // loads per step
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   __shared__ SchedLds sl;
 
@@ -974,7 +1027,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   const int lq = lane >> 4, lc = lane & 15;
   const int G = p.G;
   const int qbytes = G * RB;
-  const int qslot = (qbytes + 255) & ~255;
+  const int qarea = (qbytes + 255) & ~255;  // the new row (APPEND) follows q in its slot
+  const int qslot = stream_qslot(G, D, APPEND);
 
   // the per-step load count (E) must match the group: q takes exactly QD loads
   if (QD != (qbytes + 1023) / 1024) {
@@ -983,32 +1037,22 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   }
   uint8_t* wbuf = dyn + w * 4 * SB;                    // K0 V0 K1 V1
   uint8_t* qbuf = dyn + NW * 4 * SB + w * 2 * qslot;   // q slot 0, 1
+  // fused append: this wave's kept new rows (K | V per row), then their rows
+  uint8_t* sbuf = dyn + NW * (4 * SB + 2 * qslot) + w * kSaveRows * (2 * RB + 8);
+  int64_t* srow = (int64_t*)(sbuf + kSaveRows * 2 * RB);
+  int nsaved = 0;
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_address(wbuf));
   const uint32_t lds_q = __builtin_amdgcn_readfirstlane(lds_address(qbuf));
   const T* kp = (const T*)p.k;
   const T* vp = (const T*)p.v;
   // rows [row0, row0 + nrows) of K or V into step buffer b, 16-byte chunks
   // swizzled by the row (K: chunk ^ (r % CH); V: chunk ^ 2 (r % 4)); rows past
-  // nrows repeat the last row.  news >= 0 (APPEND): the last row is segment
-  // news's new row, read from new_k / new_v (the pool does not hold it yet).
-  auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b, int news) {
+  // nrows repeat the last row
+  auto load_rows = [&](bool is_v, int64_t row0, int nrows, int b) {
     // wave-uniform addresses, kept scalar (the load takes them in SGPRs)
     const T* src = (const T*)uni((int64_t)(uintptr_t)((is_v ? vp : kp) + row0 * D));
     const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_w + b * 2 * SB + (is_v ? SB : 0));
     nrows = uni((int32_t)nrows);
-    if (APPEND && news >= 0) {  // wave-uniform; the same number of loads either way
-      const uint8_t* nsrc = (const uint8_t*)(is_v ? p.new_v : p.new_k) + (int64_t)news * RB;
-#pragma unroll
-      for (int u = 0; u < NI; ++u) {
-        const int r = u * RPI + lane / CH;
-        const int rr = max(0, r < nrows ? r : nrows - 1);
-        const int sw = is_v ? 2 * (r & 3) : r % CH;
-        const int chunk = ((lane % CH) ^ sw) * 16;
-        const uint8_t* a = rr == nrows - 1 ? nsrc + chunk : (const uint8_t*)src + rr * RB + chunk;
-        dma_copy16_a64(a, dst + u * 1024);
-      }
-      return;
-    }
 #pragma unroll
     for (int u = 0; u < NI; ++u) {
       const int r = u * RPI + lane / CH;
@@ -1084,10 +1128,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
         llo = lo;
         llen = hi - lo;
         lneg = llen < 0;
-        if (APPEND) {
-          lcap = p.cap[s];
-          if (!lneg) ++llen;
-        }
+        if (APPEND) lcap = p.cap[s];
         if (XL && p.xmask[s % p.Hkv]) {
           la0 = p.audio_s[s / p.Hkv];
           lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
@@ -1098,13 +1139,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   };
   load_window(!direct);
   if (direct) {
-    // The rows the split covers end at cu[n_seg] (+ n_seg with APPEND):
-    // lane n_seg - 1 holds it.  Read from the table rather than passed in,
-    // so a launch captured in a graph stays right as the segments grow.
-    // Only this wave's own bounds sit on the start-up path; the
-    // workgroup's follow once the first steps are issued.
-    const int32_t lhi = APPEND && !lneg ? llo + llen - 1 : llo + llen;  // cu[s + 1]
-    R = max((int64_t)0, (int64_t)__builtin_amdgcn_readlane(lhi, p.n_seg - 1) + (APPEND ? p.n_seg : 0));
+    // The rows the split covers end at cu[n_seg]: lane n_seg - 1 holds it.
+    // Read from the table rather than passed in, so a launch captured in a
+    // graph stays right as the segments grow.  Only this wave's own bounds
+    // sit on the start-up path; the workgroup's follow once the first steps
+    // are issued.
+    R = max((int64_t)0, (int64_t)__builtin_amdgcn_readlane(llo + llen, p.n_seg - 1));
     P_ = effective_wgs(R);
     if ((int64_t)blockIdx.x < P_) {
       W0 = split_start((int64_t)blockIdx.x * NW + w, R, P_, p.split_inv);
@@ -1113,7 +1153,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     window_mask();
   }
   // issue-side iterator: current piece [pb, pe) of segment cur_s (logical rows)
-  int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0, cur_wr = 0;
+  int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0, cur_k = 0;
   int64_t cur_b = 0, cur_lo = 0, pb = 0, pe = 0, irow = 0;
   bool cur_whole = false, have = false;
   auto next_piece = [&]() {
@@ -1133,7 +1173,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
     cur_lo = __builtin_amdgcn_readlane(llo, k);
     cur_len = __builtin_amdgcn_readlane(llen, k);
-    if (APPEND) cur_wr = cur_len <= __builtin_amdgcn_readlane(lcap, k) ? 2 : 1;
+    cur_k = k;  // the segment's lane in the window (its capacity is read when its new row is folded)
     if (XL) {
       cur_a0 = __builtin_amdgcn_readlane(la0, k);
       cur_al = __builtin_amdgcn_readlane(lal, k);
@@ -1159,7 +1199,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       st.t0 = (int32_t)(irow - cur_lo) - cur_a0;
       st.alen = cur_al;
     }
-    st.newrow = APPEND && irow + st.nrows == cur_lo + cur_len ? cur_wr : 0;
+    st.ends_seg = APPEND && irow + st.nrows == cur_lo + cur_len;
+    st.wr = cur_k;
     irow += kSRows;
     st.last = irow >= pe;
     if (st.last) {
@@ -1169,11 +1210,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     return true;
   };
 
-  // ---- loads of one step into buffer b: K, q, V (E loads, in this order)
-  // q is loaded for the first step of a piece only (the later steps keep it
-  // in registers), so a step issues E loads with q and E - QD without.
+  // ---- loads of one step into buffer b: K, q (+ new row), V (E loads, in
+  // this order).  q is loaded for the first step of a piece only (the later
+  // steps keep it in registers), so a step issues E loads with q and E - QX
+  // without.  With the fused append the first step also copies the
+  // segment's new K and V rows behind q (lanes 0 .. CH-1: K chunks, CH ..
+  // 2CH-1: V chunks, the others repeat them), one 64-bit-addressed load.
   auto issue = [&](const SStep& st, int b) {
-    load_rows(false, st.row0, st.nrows, b, st.newrow ? st.s : -1);
+    load_rows(false, st.row0, st.nrows, b);
     if (st.first) {
       const T* qs = (const T*)uni((int64_t)(uintptr_t)((const T*)p.q + (int64_t)st.s * G * D));
 #pragma unroll
@@ -1182,8 +1226,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
         if (off < qbytes)
           dma_copy16(qs, (uint32_t)off, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + u * 1024));
       }
+      if (APPEND) {
+        const int c = lane % (2 * CH);
+        const uint8_t* a = (const uint8_t*)(c < CH ? p.new_k : p.new_v) + (int64_t)st.s * RB + (c % CH) * 16;
+        dma_copy16_a64(a, __builtin_amdgcn_readfirstlane(lds_q + st.qslot * qslot + qarea));
+      }
     }
-    load_rows(true, st.row0, st.nrows, b, st.newrow ? st.s : -1);
+    load_rows(true, st.row0, st.nrows, b);
   };
 
   // ---- softmax state of the current piece, and the held (first, shared) one
@@ -1202,6 +1251,61 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   int64_t c_b = 0;
   u32x4 qb[NC];
 
+  // APPEND, a segment whose last step is full (16 old rows): its new row
+  // (behind q in the piece's slot) folded into the softmax state once the
+  // step is done -- one more logit per head (the dot product of q's chunks in
+  // this lane with the row's, summed over the head's four lanes) and one more
+  // V row (this lane's accumulator elements 16 t + 4 lq + i).  Every LDS read
+  // is issued before the math.  (A last step with room takes the row as one
+  // of its own rows instead; see process.)
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  auto fold_new_row = [&](const SStep& st) {
+    const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;  // K row, then V row
+    u32x4 kk[NC];
+    u32x2 vv[NTD];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) kk[c] = *(const u32x4*)(nrow + (4 * c + lq) * 16);
+#pragma unroll
+    for (int t = 0; t < NTD; ++t) vv[t] = *(const u32x2*)(nrow + RB + (16 * t + 4 * lq) * 2);
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dot += Ops::to_f32(qb[c][j] & 0xffffu) * Ops::to_f32(kk[c][j] & 0xffffu) +
+               Ops::to_f32(qb[c][j] >> 16) * Ops::to_f32(kk[c][j] >> 16);
+    dot = sum_x32(sum_x16(dot));
+    const float xn = lc < G ? dot * p.scale_log2 : -INFINITY;
+    const float m_new = fmaxf(m_run, xn);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float pw = __builtin_amdgcn_exp2f(xn - m_new);
+    m_run = m_new;
+    l_run = l_run * alpha + (lq == 0 ? pw : 0.f);
+#pragma unroll
+    for (int t = 0; t < NTD; ++t) {
+      acc[t][0] = acc[t][0] * alpha + pw * Ops::to_f32(vv[t].x & 0xffffu);
+      acc[t][1] = acc[t][1] * alpha + pw * Ops::to_f32(vv[t].x >> 16);
+      acc[t][2] = acc[t][2] * alpha + pw * Ops::to_f32(vv[t].y & 0xffffu);
+      acc[t][3] = acc[t][3] * alpha + pw * Ops::to_f32(vv[t].y >> 16);
+    }
+  };
+  // APPEND: a segment's new row kept for the pools (stored after the hand-off)
+  // when the segment has room for it; the capacity, loaded with the table,
+  // is read only now.  The row goes after the segment's old rows.
+  auto keep_new_row = [&](const SStep& st) {
+    if (st.seg_len + 1 > __builtin_amdgcn_readlane(lcap, st.wr)) return;  // wave-uniform
+    const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;
+    const int64_t row = st.row0 + st.nrows;
+    if (nsaved < kSaveRows) {  // wave-uniform
+      if (lane < 2 * CH) *(u32x4*)(sbuf + nsaved * 2 * RB + lane * 16) = *(const u32x4*)(nrow + lane * 16);
+      if (lane == 0) srow[nsaved] = row;
+      ++nsaved;
+    } else if (lane < 2 * CH) {  // keep-list full: stored now (its acknowledgement delays the next wait)
+      *(WNW_GLOBAL u32x4*)(gptr_w<uint8_t>(const_cast<void*>(lane < CH ? p.k : p.v)) + row * RB +
+                           (lane % CH) * 16) = *(const u32x4*)(nrow + lane * 16);
+    }
+  };
+
   auto process = [&](const SStep& st, int b, bool has_next, bool next_first) {
     uint8_t* kbuf = wbuf + b * 2 * SB;
     uint8_t* vbuf = kbuf + SB;
@@ -1210,7 +1314,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     if (has_next && next_first)
       wait_vmcnt<NI + E>();
     else if (has_next)
-      wait_vmcnt<NI + E - QD>();
+      wait_vmcnt<NI + E - QX>();
     else
       wait_vmcnt<NI>();
     __builtin_amdgcn_sched_barrier(0);
@@ -1220,6 +1324,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       for (int c = 0; c < NC; ++c)
         qb[c] = lc < G ? *(const u32x4*)(qsl + lc * RB + (4 * c + lq) * 16) : u32x4{0, 0, 0, 0};
     }
+    // APPEND: a step that ends its segment with fewer than 16 old rows takes
+    // the segment's new row (behind q in the piece's slot) as row nrows:
+    // its K chunks now, swizzled like the loaded rows, its V chunks after
+    // V's wait.  The step's DMA has landed, and the buffer is this wave's
+    // until the step after next is issued.
+    const bool add_row = APPEND && st.ends_seg && st.nrows < kSRows;  // wave-uniform
+    if (add_row && lane < CH) {
+      const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;
+      *(u32x4*)(kbuf + st.nrows * RB + ((lane ^ (st.nrows % CH)) * 16)) = *(const u32x4*)(nrow + lane * 16);
+    }
+    const int nvalid = st.nrows + (add_row ? 1 : 0);
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1231,7 +1346,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     float mx = kNegBig;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      x[i] = (4 * lq + i) < st.nrows ? sacc[i] * p.scale_log2 : -INFINITY;
+      x[i] = (4 * lq + i) < nvalid ? sacc[i] * p.scale_log2 : -INFINITY;
       mx = fmaxf(mx, x[i]);
     }
     if (XL && st.alen > 0 && st.t0 < st.alen && st.t0 + st.nrows > 0 && lc < G) {
@@ -1270,10 +1385,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     if (has_next && next_first)
       wait_vmcnt<E>();
     else if (has_next)
-      wait_vmcnt<E - QD>();
+      wait_vmcnt<E - QX>();
     else
       wait_vmcnt<0>();
     __builtin_amdgcn_sched_barrier(0);
+    if (add_row && lane < CH) {  // the new row's V chunks as row nrows
+      const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;
+      *(u32x4*)(vbuf + st.nrows * RB + ((lane ^ (2 * (st.nrows & 3))) * 16)) =
+          *(const u32x4*)(nrow + RB + lane * 16);
+    }
     // V^T operand of tile t: lane (lq, lc) addresses row 4 lq + lc / 4, columns
     // 16 t + 4 (lc % 4) .. + 3 (8 bytes of the swizzled row)
     {
@@ -1289,22 +1409,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (APPEND && st.newrow == 2) {
-      // the segment's new row (the step's last row, read from new_k / new_v)
-      // goes into the pool from LDS: lanes 0 .. CH-1 write its K chunks,
-      // CH .. 2CH-1 its V chunks (un-swizzled); no other wave reads that
-      // pool row in this launch
-      const int r = st.nrows - 1;
-      if (lane < 2 * CH) {
-        const bool isv = lane >= CH;
-        const int c = lane % CH;
-        const int sw = isv ? 2 * (r & 3) : r % CH;
-        const u32x4 d = *(const u32x4*)((isv ? vbuf : kbuf) + r * RB + (c ^ sw) * 16);
-        WNW_GLOBAL uint8_t* dst = gptr_w<uint8_t>(const_cast<void*>(isv ? p.v : p.k)) + (st.row0 + r) * RB + c * 16;
-        *(WNW_GLOBAL u32x4*)dst = d;
-      }
-    }
     if (st.last) {
+      if (APPEND && st.ends_seg) {
+        if (!add_row) fold_new_row(st);
+        keep_new_row(st);
+      }
       const float l_tot = sum_x32(sum_x16(l_run));
       if (st.whole) {  // the segment lies inside this wave's range: finish it
         if (lc < G) {
@@ -1368,24 +1477,19 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   if (direct && w == 0) {
     const int si = lane;
     const bool in = si < p.n_seg;
-    // llen already counts the new row with APPEND, unless the offsets
-    // decrease (lneg: a corrupt table, treated as an empty segment)
+    // lneg: the offsets of this segment decrease (a corrupt table, treated
+    // as an empty segment)
     const int64_t len = in && !lneg ? llen : 0;
     const bool bad = in && lneg;
     if (bad) raise_device_error(p.err, WNW_DEVERR_ORDER);
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) sl.order_bad = any_bad;
-    if (APPEND && in) {
-      if (!lneg && len > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
-      if (blockIdx.x == 0) {  // post-append offsets: cu_out = cu + arange(n_seg + 1)
-        WNW_GLOBAL int32_t* co = gptr_w<int32_t>(p.cu_out);
-        co[si] = llo + si;
-        if (si == p.n_seg - 1) co[p.n_seg] = llo + llen - (lneg ? 0 : 1) + p.n_seg;
-      }
-    }
     if (in && !seg_valid(llo, len, lb, R, KV)) {
+      const bool owner = (si % (int)gridDim.x) == (int)blockIdx.x;
       if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
-      if ((si % (int)gridDim.x) == (int)blockIdx.x) {
+      if (APPEND && len == 0 && !lneg) {  // only the new row: it is the output
+        if (owner) append_only_segment<T>(p, D, si, lb, 1 <= lcap && lb >= 0 && lb < KV);
+      } else if (owner) {
         const float fill = len == 0 ? 0.f : __int_as_float(0x7fc00000);
         for (int e = 0; e < G * D; ++e) store_elem<T>(p.out, (int64_t)si * G * D + e, fill);
         if (p.lse) {
@@ -1573,6 +1677,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     if (tid == 0) sl.is_last = (int)(fl & 3);
   }
   __syncthreads();
+  if (APPEND) {
+    // the kept new rows into the pools: no wait of this workgroup follows
+    // (the combine below reads other memory), so their acknowledgement
+    // overlaps the combine
+    for (int i = 0; i < nsaved; ++i) {
+      const int64_t row = uni(srow[i]);
+      if (lane < 2 * CH)
+        *(WNW_GLOBAL u32x4*)(gptr_w<uint8_t>(const_cast<void*>(lane < CH ? p.k : p.v)) + row * RB +
+                             (lane % CH) * 16) = *(const u32x4*)(sbuf + i * 2 * RB + lane * 16);
+    }
+  }
   // the segments this workgroup completes are merged side by side (one
   // half of the workgroup each when there are two)
   const int last = uni(sl.is_last);
@@ -1581,6 +1696,16 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     const int nt = both ? NT / 2 : NT;
     const bool k = both ? tid >= NT / 2 : last == 2;  // uniform per wave
     combine_from<T>(p, D, k ? pf1 : pf0, (k ? pn1 : pn0) + 1, k ? ps1 : ps0, both && k ? tid - NT / 2 : tid, nt);
+  }
+  if (APPEND) {
+    // (direct table) workgroup 0's post-append offsets, last, so no wait of
+    // this kernel waits for them, and the capacity check of every segment
+    if (direct && blockIdx.x == 0 && w == 0 && lane < p.n_seg) {  // cu_out = cu + arange(n_seg + 1)
+      WNW_GLOBAL int32_t* co = gptr_w<int32_t>(p.cu_out);
+      co[lane] = llo + lane;
+      if (lane == p.n_seg - 1) co[p.n_seg] = llo + llen + p.n_seg;  // llen: cu[s + 1] - cu[s], as read
+      if (!lneg && llen + 1 > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
+    }
   }
 }
 
@@ -1807,12 +1932,12 @@ static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex&
 // and device).
 template <typename T, int D, int QD, bool XL, bool APPEND>
 static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
-  const int qslot = (ap.G * D * 2 + 255) & ~255;
-  const int lds = stream_lds_bytes(D, kNW, qslot);
+  const int lds = stream_lds_bytes(D, kNW, stream_qslot(ap.G, D, APPEND), APPEND);
   static std::mutex mu;
   static std::vector<signed char> done;
-  const hipError_t attr_err = set_lds_limit_once(
-      done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND>, stream_lds_bytes(D, kNW, 2048));
+  const hipError_t attr_err =
+      set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND>,
+                         stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND));
   if (attr_err != hipSuccess) return attr_err;
   hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
                      st, ap.q, ap.k, ap.v, ap.cu, ap.base, ap.split_inv, ap.n_seg, ap.G, ap);

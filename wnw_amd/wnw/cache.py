@@ -5,9 +5,15 @@ hook; every device operation is a kernel of ``libwnw_amd.so`` and every
 planning decision the native planner (``wnw_amd.wnw_cpp.planner``):
 
 decode step, per layer (cache.py:487-566)
-    ``decode_before_attn``      append (``interleave_append``), or the pending
-                                compaction + load + append
-                                (``rebuild_append_kv``) when a plan is active;
+    ``decode_step_attention``   the decode branch of the patched forward in
+                                one call: a pending plan's compaction of the
+                                changed segments, then the step's append
+                                fused into the attention launch (with the
+                                class-A scores of a foldable layer);
+    ``decode_before_attn``      the reference's hook: the pending compaction,
+                                then the append alone (in place; or
+                                ``interleave_append`` / ``rebuild_append_kv``
+                                on the dense layout);
     ``fused_decode_attention``  foldable class-A layer: attention + scores in
                                 one operator (``q1_decode_attn_score``), else
                                 attention then ``decode_after_attn``;
@@ -26,6 +32,20 @@ text; the pruned audio rows of class-B heads go to pinned host memory,
 grouped per (layer, sample, head, segment) (``restore_meta``), and the
 initial top-k chunks are loaded back.
 
+Layout.  With ``slack_rows`` > 0 (the default, 256) each layer is a pool
+in which segment s owns ``seg_cap[s]`` rows from physical row
+``seg_base[s]``: its ``len`` rows, then room for the next appends.  The
+logical view is the reference's (``cu_seqlens_k``, ``seq_lens``, row order
+within a segment); only the physical placement differs, so every attention
+launch takes ``seg_base``, and ``dense_kv(layer)`` gathers the reference's
+dense rows for a caller that needs them.  Appends are in place (one row per
+segment, no copy of the layer).  A plan's changed segments are compacted
+into the pool's free tail (relocated; the old rows are left behind), and
+only when the tail is used up is the layer copied into a fresh pool.
+``slack_rows=0`` keeps the reference's dense layout, where every append
+copies the layer out of place (``interleave_append``) and every plan
+rebuilds it (``rebuild_append_kv``).
+
 One deliberate difference: before the host refills the pinned staging
 buffer for a new plan it waits for the previous plan's H2D copy (the
 reference overwrites staging that an in-flight copy may still read).
@@ -42,11 +62,11 @@ from torch import Tensor
 
 from .. import _lib
 from ..kv.flat_cache import FlatVarlenCache
-from ..kv.fused_attn import q1_decode_attn, q1_decode_attn_score
-from ..kv.kernels import interleave_append
+from ..kv.fused_attn import decode_attn, q1_decode_attn, q1_decode_attn_score
+from ..kv.kernels import append_inplace, interleave_append
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
-from .kernels import fused_score_accumulate, gather_host_rows, host_rows_readable, rebuild_append_kv
+from .kernels import compact_segments, fused_score_accumulate, gather_host_rows, host_rows_readable, rebuild_append_kv
 
 
 @dataclass
@@ -78,6 +98,10 @@ def _build_cu_seqlens(seq_lens: list[int], device: torch.device) -> Tensor:
 
 def _build_cu_seqlens_list(seq_lens: list[int]) -> list[int]:
     return [0] + list(accumulate(seq_lens))
+
+
+def _round8(n: int) -> int:
+    return (n + 7) // 8 * 8
 
 
 def _select_topk_per_segment(scores: Tensor, seg_ranges: list[tuple[int, int]], ratio: float) -> Tensor:
@@ -113,8 +137,22 @@ class WnWCache(FlatVarlenCache):
     """WnW KV cache manager (see the module docstring for the step flow)."""
 
     def __init__(self, config: WnWConfig, num_layers: int, num_kv_heads: int, num_q_heads: int, head_dim: int,
-                 device: torch.device, adapter=None):
+                 device: torch.device, adapter=None, slack_rows: int | None = None):
         super().__init__(num_layers, num_kv_heads, num_q_heads, head_dim, device, adapter)
+        # spare rows per segment for in-place appends (WNW_SLACK_ROWS, default
+        # 256); 0 keeps the reference's dense layout
+        if slack_rows is None:
+            slack_rows = int(os.environ.get("WNW_SLACK_ROWS", "256"))
+        if slack_rows < 0:
+            raise ValueError("slack_rows must be >= 0")
+        self.slack_rows = int(slack_rows)
+        # free tail of a pool with host rows: max(tail_rows_min, tail_factor x
+        # the class-B rows), the room for segments a plan relocates
+        self.tail_rows_min = 1024
+        self.tail_factor = 2
+        # layout changes so far: (fresh pools, fresh pools applying a plan,
+        # plans applied by relocating segments into the tail)
+        self.layout_counts = {"relayout": 0, "relayout_plan": 0, "relocate": 0}
         if config.num_layers == 0:
             config.set_model_dims(num_layers, num_kv_heads, num_q_heads)
         self.config = config
@@ -124,6 +162,7 @@ class WnWCache(FlatVarlenCache):
         self.cu_seqlens_k: list[Tensor | None] = [None] * num_layers
         self.cu_seqlens_list: list[list[int] | None] = [None] * num_layers
         self.seq_lens: list[list[int] | None] = [None] * num_layers
+        self._reset_layout_state()
         self.cpu_restore_k: Tensor | None = None
         self.cpu_restore_v: Tensor | None = None
         self.restore_meta: list = []
@@ -185,6 +224,7 @@ class WnWCache(FlatVarlenCache):
         self.cu_seqlens_k = [None] * L
         self.cu_seqlens_list = [None] * L
         self.seq_lens = [None] * L
+        self._reset_layout_state()
         self.restore_meta = [[[[None] * len(self.segment_ranges[b]) for _ in range(H)] for b in range(B)]
                              for _ in range(L)]
         self._cpu_buffers_k, self._cpu_buffers_v, self._cpu_buffer_metas = [], [], []
@@ -192,6 +232,22 @@ class WnWCache(FlatVarlenCache):
         self._decode_step = 0
         self._planner = None
         self._clear_pending_rebuild_state()
+
+    @property
+    def slack_layout(self) -> bool:
+        return self.slack_rows > 0
+
+    def _reset_layout_state(self) -> None:
+        L = self.num_layers
+        self.seg_base: list[Tensor | None] = [None] * L   # int64 [N] physical first row (slack layout)
+        self.seg_cap: list[Tensor | None] = [None] * L    # int32 [N] rows each segment may occupy
+        self._base_list: list[list[int] | None] = [None] * L
+        self._cap_list: list[list[int] | None] = [None] * L
+        self._cu_spare: list[Tensor | None] = [None] * L  # the offsets buffer the next append writes
+        self._headroom = [0] * L                          # min over segments of cap - len
+        self._tail = [0] * L                              # first free row after the segments
+        self._max_len = [0] * L
+        self._rows = [0] * L                              # sum of the segment lengths
 
     def _clear_pending_rebuild_state(self) -> None:
         L = self.num_layers
@@ -288,6 +344,7 @@ class WnWCache(FlatVarlenCache):
             self._select_and_apply_chunks(b, avg)
             self._prefill_scores[b].clear()
         self.prefilled = True
+        self._to_slack_layout()
         self._init_planner()
         self._precompute_decode_constants()
         self.stats.record_prefill(self._snapshot_cache_stats)
@@ -309,6 +366,7 @@ class WnWCache(FlatVarlenCache):
         self.restore_meta = restore_meta
         self.loaded_segments = [set(s) for s in loaded_segments]
         self.prefilled = True
+        self._to_slack_layout()
         self._init_planner()
         self._precompute_decode_constants()
 
@@ -370,6 +428,96 @@ class WnWCache(FlatVarlenCache):
             self.seq_lens[l] = lens
             self.cu_seqlens_k[l] = _build_cu_seqlens(lens, self.device)
             self.cu_seqlens_list[l] = _build_cu_seqlens_list(lens)
+
+    # ----------------------------------------------------------------- layout
+    def _to_slack_layout(self) -> None:
+        """After prefill: every layer's dense rows into a pool with slack."""
+        N = self.batch_size * self.num_kv_heads
+        self._all_segs = torch.arange(N, dtype=torch.int32, device=self.device)
+        self._no_loads = torch.full((N,), -1, dtype=torch.int32, device=self.device)
+        self._zeros_n = torch.zeros(N, dtype=torch.int32, device=self.device)
+        self._zeros_n1 = torch.zeros(N + 1, dtype=torch.int32, device=self.device)
+        self._empty_i32 = torch.empty(0, dtype=torch.int32, device=self.device)
+        for l in range(self.num_layers):
+            self._rows[l] = sum(self.seq_lens[l])
+            self._max_len[l] = max(self.seq_lens[l], default=0)
+            if self.slack_layout:
+                self._relayout(l)
+
+    def _tail_rows(self, layer_idx: int, lens: list[int]) -> int:
+        """Free rows kept after the segments, for segments a plan changes
+        (relocated there with their slack): ``tail_factor`` times the room
+        the layer's class-B segments take, at least ``tail_rows_min``, when
+        there are host rows to load, else none (no plan changes a layout
+        without them)."""
+        if self.cpu_restore_k is None or self.cpu_restore_k.shape[0] == 0:
+            return 0
+        H = self.num_kv_heads
+        heads = set(self._class_b_heads_by_layer[layer_idx])
+        room = sum(_round8(n + self.slack_rows) for f, n in enumerate(lens) if f % H in heads)
+        return _round8(max(self.tail_rows_min, self.tail_factor * room))
+
+    def _relayout(self, layer_idx: int, plan: dict | None = None) -> None:
+        """Copy layer ``layer_idx`` into a fresh pool: every segment's rows in
+        index order with ``slack_rows`` of room after each, then a free tail.
+        The source is the current pool (or the dense layer right after
+        prefill).  With ``plan`` (the layer's compaction descriptors) the
+        evictions and loads are applied on the way, to the plan's lengths
+        without the step's append."""
+        l, dev, D = layer_idx, self.device, self.head_dim
+        N = self.batch_size * self.num_kv_heads
+        new_lens = list(self.seq_lens[l]) if plan is None else list(plan["lens"])
+        caps = [_round8(n + self.slack_rows) for n in new_lens]
+        bases = [0] + list(accumulate(caps))[:-1]
+        used = sum(caps)
+        pool = used + self._tail_rows(l, new_lens)
+        cu = self.cu_seqlens_k[l]
+        src_base = self.seg_base[l] if self.seg_base[l] is not None else cu[:-1].to(torch.int64)
+        src_len = cu[1:] - cu[:-1]
+        dst_base = torch.tensor(bases, dtype=torch.int64, device=dev)
+        new_len_t = torch.tensor(new_lens, dtype=torch.int32, device=dev)
+        old_k, old_v = self.layer_k[l], self.layer_v[l]
+        k = torch.empty(pool, D, dtype=old_k.dtype, device=dev)
+        v = torch.empty_like(k)
+        if max(new_lens, default=0) > 0:
+            if plan is None:
+                compact_segments(old_k, old_v, k, v, self._all_segs, src_base, src_len, dst_base, new_len_t,
+                                 old_k[:0], old_v[:0], self._no_loads, self._zeros_n, self._zeros_n1,
+                                 self._empty_i32, self._empty_i32, max(new_lens))
+            else:
+                compact_segments(old_k, old_v, k, v, self._all_segs, src_base, src_len, dst_base, new_len_t,
+                                 plan["load_k"], plan["load_v"], plan["load_starts"], plan["load_lens"],
+                                 plan["evict_offsets"], plan["evict_starts"], plan["evict_ends"], max(new_lens))
+        self.layer_k[l], self.layer_v[l] = k, v
+        self.seg_base[l] = dst_base
+        self.seg_cap[l] = torch.tensor(caps, dtype=torch.int32, device=dev)
+        self._base_list[l], self._cap_list[l] = bases, caps
+        self._tail[l] = used
+        self._set_lens(l, new_lens)
+        self.layout_counts["relayout" if plan is None else "relayout_plan"] += 1
+
+    def _set_lens(self, layer_idx: int, lens: list[int]) -> None:
+        """Host lengths and device offsets of a layer after a layout change."""
+        l = layer_idx
+        self.seq_lens[l] = list(lens)
+        self.cu_seqlens_list[l] = _build_cu_seqlens_list(self.seq_lens[l])
+        self.cu_seqlens_k[l] = torch.tensor(self.cu_seqlens_list[l], dtype=torch.int32, device=self.device)
+        self._cu_spare[l] = torch.empty_like(self.cu_seqlens_k[l])
+        self._rows[l] = self.cu_seqlens_list[l][-1]
+        self._max_len[l] = max(lens, default=0)
+        self._headroom[l] = min((c - n for c, n in zip(self._cap_list[l], lens)), default=0)
+
+    def dense_kv(self, layer_idx: int) -> tuple[Tensor, Tensor]:
+        """The layer's rows in the reference's dense layout (segment s at
+        rows [cu[s], cu[s+1]) of [total, head_dim]); a gather on the slack
+        layout, the layer itself on the dense one."""
+        l = layer_idx
+        if self.seg_base[l] is None:
+            return self.layer_k[l], self.layer_v[l]
+        idx = torch.cat([torch.arange(b, b + n, device=self.device)
+                         for b, n in zip(self._base_list[l], self.seq_lens[l])]) if self._rows[l] else \
+            torch.empty(0, dtype=torch.int64, device=self.device)
+        return self.layer_k[l].index_select(0, idx), self.layer_v[l].index_select(0, idx)
 
     def _init_planner(self) -> None:
         """Hand segments, chunks, class-B heads, restore metadata, loaded sets
@@ -477,8 +625,27 @@ class WnWCache(FlatVarlenCache):
         self._tk_k = min(self.config.top_k_chunks, self._max_chunks)
 
     # ----------------------------------------------------------------- decode
+    def _before_decode_layer(self, layer_idx: int) -> None:
+        """Work due before a layer's decode step (the deferred-plan variant
+        finalises its plan at layer 0)."""
+
     def decode_before_attn(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
-        """cache.py:487-515: returns (K, V, cu_seqlens_k, max_seqlen_k)."""
+        """cache.py:487-515: returns (K, V, cu_seqlens_k, max_seqlen_k).
+
+        Slack layout: K and V are the layer's pools and segment s's rows
+        start at physical row ``seg_base[layer_idx][s]``; the append is in
+        place.  Dense layout: the reference's arrays, rebuilt out of place."""
+        self._before_decode_layer(layer_idx)
+        if self.slack_layout:
+            l = layer_idx
+            self._apply_pending_slack(l)
+            self._ensure_headroom(l)
+            nk = new_k.squeeze(2).reshape(-1, self.head_dim)
+            nv = new_v.squeeze(2).reshape(-1, self.head_dim)
+            append_inplace(self.layer_k[l], self.layer_v[l], nk, nv, self.cu_seqlens_k[l], self._cu_spare[l],
+                           self.seg_base[l], self.seg_cap[l])
+            self._commit_append(l)
+            return self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], self._max_len[l]
         if self._pending_chunk_update:
             if self.use_triton_rebuild and self._pending_cu_new[layer_idx] is not None:
                 return self._rebuild_append_layer(layer_idx, new_k, new_v)
@@ -494,7 +661,151 @@ class WnWCache(FlatVarlenCache):
         self.seq_lens[layer_idx] = new_lens
         self.cu_seqlens_k[layer_idx] = cu_new
         self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(new_lens)
+        self._rows[layer_idx] += len(new_lens)
+        self._max_len[layer_idx] = max(new_lens)
         return k, v, cu_new, max(new_lens)
+
+    def decode_step_attention(self, layer_idx: int, q_flat: Tensor, q: Tensor, new_k: Tensor, new_v: Tensor,
+                              scale: float, fused: bool) -> Tensor:
+        """The decode branch of the patched forward (session.py:78-116) from
+        the append on: ``decode_before_attn`` + the attention (+ scores), in
+        as few launches as the layout allows.  Slack layout: a pending plan's
+        compaction of the changed segments, then one launch that appends the
+        step's row to every segment and attends (with the class-A scores of a
+        foldable layer when ``fused``, as ``fused_decode_attention`` does);
+        other class-A layers score afterwards (``decode_after_attn``).
+        Returns the attention output [N, G, D]."""
+        l = layer_idx
+        if not self.slack_layout:
+            k, v, cu, _ = self.decode_before_attn(l, new_k, new_v)
+            if fused:
+                return self.fused_decode_attention(l, q_flat, q, k, v, cu, scale)
+            out = q1_decode_attn(q_flat, k, v, cu, scale)
+            self.decode_after_attn(l, q)
+            return out
+        self._before_decode_layer(l)
+        self._apply_pending_slack(l)
+        self._ensure_headroom(l)
+        nk = new_k.squeeze(2).reshape(-1, self.head_dim)
+        nv = new_v.squeeze(2).reshape(-1, self.head_dim)
+        app = (nk, nv, self._cu_spare[l], self.seg_cap[l])
+        rows = self._rows[l] + self.batch_size * self.num_kv_heads
+        score_here = fused and self._layer_foldable[l]
+        if score_here:
+            out = q1_decode_attn_score(q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale,
+                                       self._ca_kv_mask_by_layer[l], self.num_kv_heads, self._decode_audio_starts_b,
+                                       self._decode_audio_ends_b, self.score_accumulator, self.score_offsets,
+                                       seg_base=self.seg_base[l], total_rows=rows, max_audio=self._max_audio,
+                                       append=app)
+        else:
+            out = decode_attn(q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale,
+                              seg_base=self.seg_base[l], total_rows=rows, append=app)
+        self._commit_append(l)
+        if not score_here:
+            self.decode_after_attn(l, q)
+        return out
+
+    def _commit_append(self, layer_idx: int) -> None:
+        """Host bookkeeping of an in-place append: the offsets the append
+        wrote become current, every segment is one row longer."""
+        l = layer_idx
+        self.cu_seqlens_k[l], self._cu_spare[l] = self._cu_spare[l], self.cu_seqlens_k[l]
+        self.seq_lens[l] = [x + 1 for x in self.seq_lens[l]]
+        self.cu_seqlens_list[l] = None  # rebuilt on demand (cu_list)
+        self._headroom[l] -= 1
+        self._max_len[l] += 1
+        self._rows[l] += len(self.seq_lens[l])
+
+    def decode_headroom(self) -> int:
+        """Decode steps every layer can still append in place (slack layout)
+        before a pool is rebuilt: the most steps a captured graph of plain
+        decode steps may be replayed for."""
+        return min(self._headroom) if self.slack_layout else 0
+
+    def advance_replayed_steps(self, n: int) -> None:
+        """Host bookkeeping of ``n`` decode steps that ran as replays of
+        captured graphs.  A capture runs the hooks' host side once and a
+        replay only the device work (the appends and the offsets they write),
+        so after replaying captured plain decode steps (no plan change, slack
+        layout, an even number of steps when two graphs alternate the offset
+        buffers) the host's lengths are advanced here."""
+        if n <= 0:
+            return
+        if not self.slack_layout or n > self.decode_headroom():
+            raise ValueError("replayed steps need the slack layout and room for every append")
+        for l in range(self.num_layers):
+            self.seq_lens[l] = [x + n for x in self.seq_lens[l]]
+            self.cu_seqlens_list[l] = None
+            self._headroom[l] -= n
+            self._max_len[l] += n
+            self._rows[l] += n * len(self.seq_lens[l])
+        self._decode_step += n
+        self._seq_lengths = [x + n for x in self._seq_lengths]
+
+    def cu_list(self, layer_idx: int) -> list[int]:
+        """Host copy of a layer's offsets (cu_seqlens_k)."""
+        if self.cu_seqlens_list[layer_idx] is None:
+            self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(self.seq_lens[layer_idx])
+        return self.cu_seqlens_list[layer_idx]
+
+    def _ensure_headroom(self, layer_idx: int) -> None:
+        """Room for one more row in every segment, else a fresh pool."""
+        if self._headroom[layer_idx] < 1:
+            self._relayout(layer_idx)
+
+    def _apply_pending_slack(self, layer_idx: int) -> None:
+        """A pending plan's compaction + loads for this layer (slack layout):
+        the segments the plan changes are rebuilt into the pool's free tail
+        (their old rows are left behind), or, when the tail is used up, the
+        whole layer into a fresh pool.  Lengths and offsets become the
+        plan's, without the step's append (the append follows)."""
+        l = layer_idx
+        if not self._pending_chunk_update or self._pending_cu_new[l] is None:
+            return
+        self._wait_loads(l)
+        o = self._plan_out
+        ll, eo = o["load_lens_2d"][l], o["evict_offsets_2d"][l]
+        new_lens = [x - 1 for x in self._pending_new_lens[l]]  # the append comes next
+        changed = ((ll > 0) | (eo[1:] > eo[:-1])).nonzero().flatten().tolist()
+        if changed:
+            need = sum(_round8(new_lens[s] + self.slack_rows) for s in changed)
+            plan = dict(lens=new_lens, load_k=self._pending_gpu_k, load_v=self._pending_gpu_v,
+                        load_starts=self._pending_load_starts[l], load_lens=self._pending_load_lens[l],
+                        evict_offsets=self._pending_evict_offsets[l], evict_starts=self._pending_evict_starts[l],
+                        evict_ends=self._pending_evict_ends[l])
+            if self._tail[l] + need <= self.layer_k[l].shape[0]:
+                self._relocate(l, changed, plan)
+            else:
+                self._relayout(l, plan)
+        else:
+            self._set_lens(l, new_lens)
+        self._pending_layers_applied += 1
+        if self._pending_layers_applied == self.num_layers:
+            self._pending_chunk_update = False
+            self._clear_pending_rebuild_state()
+
+    def _relocate(self, layer_idx: int, changed: list[int], plan: dict) -> None:
+        """The changed segments, compacted with their loads, into fresh rows
+        of the pool's free tail (disjoint from every segment's rows)."""
+        l, dev = layer_idx, self.device
+        bases, caps = list(self._base_list[l]), list(self._cap_list[l])
+        t = self._tail[l]
+        for s in changed:
+            bases[s], caps[s] = t, _round8(plan["lens"][s] + self.slack_rows)
+            t += caps[s]
+        cu = self.cu_seqlens_k[l]
+        dst_base = torch.tensor(bases, dtype=torch.int64, device=dev)
+        k, v = self.layer_k[l], self.layer_v[l]
+        compact_segments(k, v, k, v, torch.tensor(changed, dtype=torch.int32, device=dev), self.seg_base[l],
+                         cu[1:] - cu[:-1], dst_base, torch.tensor(plan["lens"], dtype=torch.int32, device=dev),
+                         plan["load_k"], plan["load_v"], plan["load_starts"], plan["load_lens"], plan["evict_offsets"],
+                         plan["evict_starts"], plan["evict_ends"], max(plan["lens"][s] for s in changed))
+        self.seg_base[l] = dst_base
+        self.seg_cap[l] = torch.tensor(caps, dtype=torch.int32, device=dev)
+        self._base_list[l], self._cap_list[l] = bases, caps
+        self._tail[l] = t
+        self._set_lens(l, plan["lens"])
+        self.layout_counts["relocate"] += 1
 
     def decode_after_attn(self, layer_idx: int, q: Tensor) -> None:
         """cache.py:517-544: class-A scores, each KV group against its own
@@ -503,20 +814,29 @@ class WnWCache(FlatVarlenCache):
             return
         cu = self.cu_seqlens_k[layer_idx]
         K = self.layer_k[layer_idx]
+        base = self.seg_base[layer_idx]
         for qheads, seg_idx in self._decode_after_groups[layer_idx]:
             Q = q[:, qheads, 0, :]
-            fused_score_accumulate(Q, K, cu[seg_idx].to(torch.int32), cu[seg_idx + 1].to(torch.int32),
-                                   self._decode_audio_starts_b, self._decode_audio_ends_b, self.score_accumulator,
-                                   self.score_offsets, max_audio=self._max_audio)
+            lo, hi = cu[seg_idx], cu[seg_idx + 1]
+            if base is None:
+                starts, ends = lo.to(torch.int32), hi.to(torch.int32)
+            else:  # physical rows of the slack layout
+                b = base[seg_idx]
+                starts, ends = b.to(torch.int32), (b + (hi - lo)).to(torch.int32)
+            fused_score_accumulate(Q, K, starts, ends, self._decode_audio_starts_b, self._decode_audio_ends_b,
+                                   self.score_accumulator, self.score_offsets, max_audio=self._max_audio)
 
     def fused_decode_attention(self, layer_idx, q_flat, q, k_flat, v_flat, cu_k, scale):
         """cache.py:546-566: foldable class-A layers score inside the
         attention operator; other class-A layers score afterwards."""
+        base = self.seg_base[layer_idx]
+        rows = self._rows[layer_idx] if base is not None else None
         if self._layer_foldable[layer_idx]:
             return q1_decode_attn_score(q_flat, k_flat, v_flat, cu_k, scale, self._ca_kv_mask_by_layer[layer_idx],
                                         self.num_kv_heads, self._decode_audio_starts_b, self._decode_audio_ends_b,
-                                        self.score_accumulator, self.score_offsets, max_audio=self._max_audio)
-        out = q1_decode_attn(q_flat, k_flat, v_flat, cu_k, scale)
+                                        self.score_accumulator, self.score_offsets, seg_base=base, total_rows=rows,
+                                        max_audio=self._max_audio)
+        out = decode_attn(q_flat, k_flat, v_flat, cu_k, scale, seg_base=base, total_rows=rows)
         self.decode_after_attn(layer_idx, q)
         return out
 

@@ -6,9 +6,10 @@ inside the ``with`` block every decoder layer's attention forward is
 replaced by one that
 * prefill: runs causal attention, computes the prefill token scores and
   hands K/V to ``cache.prefill_after_attn`` (session.py:53-76);
-* decode: appends through ``cache.decode_before_attn``, runs the gfx950
-  decode attention (``decode_attention``) and feeds the cache's scoring and
-  planning hooks (session.py:78-116).
+* decode: appends and attends through the cache (``decode_attention``: one
+  fused launch for the WnW cache, else ``cache.decode_before_attn`` and the
+  gfx950 decode attention) and feeds the cache's scoring and planning hooks
+  (session.py:78-116).
 The model-specific parts (q/k/v projections, RoPE, o_proj, locating the
 audio tokens, generate) come from the caller's adapter, exactly the methods
 the reference's adapters provide (``compute_qkv``, ``apply_rope``,
@@ -48,13 +49,18 @@ def decode_attention(cache, layer_idx: int, q: Tensor, k: Tensor, v: Tensor, sca
     B = q.shape[0]
     H, G, D = cache.num_kv_heads, cache.num_kv_groups, cache.head_dim
     cache.update(k, v, layer_idx)
-    k_flat, v_flat, cu_k, _max_k = cache.decode_before_attn(layer_idx, k, v)
     q_flat = q.squeeze(2).reshape(B, H, G, D).reshape(B * H, G, D)
-    if fused:
-        out = cache.fused_decode_attention(layer_idx, q_flat, q, k_flat, v_flat, cu_k, scaling)
+    step = getattr(cache, "decode_step_attention", None)
+    if step is not None:
+        # the WnW cache appends and attends in one launch (slack layout)
+        out = step(layer_idx, q_flat, q, k, v, scaling, fused)
     else:
-        out = q1_decode_attn(q_flat, k_flat, v_flat, cu_k, scaling)
-        cache.decode_after_attn(layer_idx, q)
+        k_flat, v_flat, cu_k, _max_k = cache.decode_before_attn(layer_idx, k, v)
+        if fused:
+            out = cache.fused_decode_attention(layer_idx, q_flat, q, k_flat, v_flat, cu_k, scaling)
+        else:
+            out = q1_decode_attn(q_flat, k_flat, v_flat, cu_k, scaling)
+            cache.decode_after_attn(layer_idx, q)
     out = out.reshape(B, H * G, D).unsqueeze(1).reshape(B, 1, H * G * D)
     if layer_idx == cache.num_layers - 1:
         cache.decode_all_layers_done()

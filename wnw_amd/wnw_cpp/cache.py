@@ -33,11 +33,11 @@ class WnWCppCache(WnWCache):
         self._topk_idx_masked = None
         super().setup_audio(audio_starts, audio_ends, attention_mask)
 
-    def decode_before_attn(self, layer_idx, new_k, new_v):
-        """wnw_cpp/code/cache.py:197-224."""
+    def _before_decode_layer(self, layer_idx):
+        """wnw_cpp/code/cache.py:197-224: the plan of the previous step's
+        scores is finalised at layer 0, before its first rebuild."""
         if not self._fallback and layer_idx == 0 and self._topk_pending:
             self._finalize_pending_plan()
-        return super().decode_before_attn(layer_idx, new_k, new_v)
 
     def _finalize_pending_plan(self) -> None:
         """wnw_cpp/code/cache.py:226-241."""

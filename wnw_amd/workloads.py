@@ -37,6 +37,8 @@ class Config:
     # kv_scale[l] : float32 [hkv]
     kv_scale: list[np.ndarray]
     notes: list[str]
+    # audio tokens per sequence (the scored rows of its class-A segments)
+    audio: np.ndarray | None = None
 
     @property
     def group(self) -> int:
@@ -78,7 +80,7 @@ def config1(seed: int = 0) -> Config:
     lens = np.array([1024 if h < 2 else 128 for _ in range(b) for h in range(hkv)], dtype=np.int64)
     ca = np.array([h < 2 for h in range(hkv)])
     return Config("cfg1-voxtral-cpu-plumbing", 1, b, 32, hkv, 128, "float32", 1, [lens], [ca],
-                  [np.ones(hkv, np.float32)], ["q, K, V ~ N(0,1), seed 0"])
+                  [np.ones(hkv, np.float32)], ["q, K, V ~ N(0,1), seed 0"], np.full(b, 1024 - 64))
 
 
 def config2(seed: int = 0, layers: int = 30) -> Config:
@@ -98,7 +100,7 @@ def config2(seed: int = 0, layers: int = 30) -> Config:
         scales.append(rng.uniform(0.5, 2.0, size=hkv).astype(np.float32))
     return Config("cfg2-voxtral-7500tok-b8", layers, b, 32, hkv, 128, "bfloat16", 128, lengths, cas, scales,
                   ["class-A count round(0.3*8)=2 per layer, heads uniform", f"seed {seed}",
-                   "class-B rows 512 before the append (compacted back each step)"])
+                   "class-B segments hold 512 rows at the start and grow by the step's row"], np.full(b, 7500))
 
 
 def config3(seed: int = 0, layers: int = 28) -> Config:
@@ -114,7 +116,7 @@ def config3(seed: int = 0, layers: int = 28) -> Config:
         cas.append(ca)
         scales.append(rng.uniform(0.5, 2.0, size=hkv).astype(np.float32))
     return Config("cfg3-qwen-omni-b16", layers, b, 28, hkv, 128, "bfloat16", 64, lengths, cas, scales,
-                  ["class-A count round(U[0.25,0.5]*4) >= 1", f"seed {seed}"])
+                  ["class-A count round(U[0.25,0.5]*4) >= 1", f"seed {seed}"], audio.astype(np.int64))
 
 
 def config5(seed: int = 0, layers: int = 30) -> Config:
@@ -133,7 +135,7 @@ def config5(seed: int = 0, layers: int = 30) -> Config:
         scales.append(rng.uniform(0.5, 2.0, size=hkv).astype(np.float32))
     return Config("cfg5-ragged-b64", layers, b, 32, hkv, 128, "bfloat16", 32, lengths, cas, scales,
                   ["lognormal sigma=1, median 3000, clip [256, 32768]", "class-A count round(U[0.1,0.6]*8) >= 1",
-                   f"seed {seed}"])
+                   f"seed {seed}"], seq.astype(np.int64))
 
 
 CONFIGS = {"cfg1": config1, "cfg2": config2, "cfg3": config3, "cfg5": config5}
