@@ -1,23 +1,20 @@
 """End-to-end decode steps through WnWCache / WnWCppCache vs a CPU simulation.
 
 The cache is prefilled through its own hooks (random K/V and tie-free
-scores), then driven through ``decode_attention`` for several steps.  The
-simulation replays every step with the oracle: appends and compactions
-(bit-exact K/V, offsets), attention (2e-3 + 1e-2 |ref|), class-A scores
-(1e-6 + 1e-3 |ref|) and the planner's loaded segments.  The chunk top-k
-that the device computes from its own float32 scores is checked against the
-oracle's ``topk_chunks(chunk_means(...))`` of the same recorded scores
-(exact unless the k-th and (k+1)-th chunk means are a float32 near-tie),
-and then fed to the oracle planner, so both sides plan from the same chunks.
+scores), then driven through ``decode_attention`` for several steps, and
+every step is checked by ``tests.cache_sim.DecodeSimulation``: appends and
+compactions (bit-exact K/V, offsets), attention (2e-3 + 1e-2 |ref|), class-A
+scores (1e-6 + 1e-3 |ref|), the device's chunk top-k against the oracle's
+``topk_chunks(chunk_means(...))`` and the planner's loaded segments; here
+also the stats record.
 """
-import copy
-
 import numpy as np
 import pytest
 import torch
 
 import oracle
 from oracle import planner as op
+from tests.cache_sim import DecodeSimulation, bits as _bits, recording as _recording
 from tests.helpers import allclose_report
 from wnw_amd import _lib
 from wnw_amd.wnw.cache import WnWCache
@@ -40,42 +37,6 @@ def _config():
                      class_b=[2, 3, H + 2, H + 3], retention_ratios=[0.5] * (L * H),
                      top_k_chunks=2, eviction_lag=2, prefill_score_mode="last",
                      num_layers=L, num_kv_heads=H, num_q_heads=HQ)
-
-
-def _recording(cls):
-    class Rec(cls):
-        def decode_all_layers_done(self):
-            self.rec_acc.append(self.score_accumulator.double().cpu().numpy().copy())
-            return super().decode_all_layers_done()
-
-        def _plan(self, topk, off):
-            o = off.tolist()
-            self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
-            return super()._plan(topk, off)
-    return Rec
-
-
-def assert_topk_matches_oracle(got_per_sample, acc, offs, bounds_per_sample, k, what=""):
-    """The device's chosen chunks of every sample equal the oracle's top-k of
-    the chunk means of ``acc`` (float64 sums over each chunk's token bounds,
-    oracle/planner.py).  A different choice is accepted only where the
-    chunks involved are within float32 rounding of the k-th largest mean
-    (the device takes float32 prefix sums)."""
-    for b, got in enumerate(got_per_sample):
-        means = op.chunk_means(acc[offs[b]:offs[b + 1]], bounds_per_sample[b])
-        want = op.topk_chunks(means, k)
-        assert len(got) == len(want) and len(set(got)) == len(got), f"{what} sample {b}: {got} vs {want}"
-        assert all(0 <= c < len(means) for c in got), f"{what} sample {b}: {got}"
-        if sorted(got) == sorted(want):
-            continue
-        kth = sorted(means, reverse=True)[len(want) - 1]
-        tol = 1e-5 * max(abs(m) for m in means) + 1e-7
-        assert all(means[c] >= kth - tol for c in got), \
-            f"{what} sample {b}: device chose {sorted(got)}, oracle {sorted(want)} (means {means})"
-
-
-def _bits(t):
-    return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
 
 def _prefill(cache, dev, gen):
@@ -125,28 +86,8 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monk
     assert _lib.device_error() == 0
     assert cache._device_gather == (not host_gather)
 
-    # simulation state, taken from the prefilled cache
-    K = [_bits(cache.dense_kv(l)[0]) for l in range(L)]
-    V = [_bits(cache.dense_kv(l)[1]) for l in range(L)]
-    lens = [list(cache.seq_lens[l]) for l in range(L)]
-    host_k, host_v = _bits(cache.cpu_restore_k), _bits(cache.cpu_restore_v)
-    meta = [[[[None if m is None else op.SegMeta(m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
-               for m in cache.restore_meta[l][b][h]] for h in range(H)] for b in range(B)] for l in range(L)]
-    loaded_after_prefill = [set(x) for x in cache.loaded_segments]
-    o = op.PlannerOracle(L, H, B, 2, 2, cache.chunk_to_segs, [cache.config.get_layer_class_b(l) for l in range(L)],
-                         meta, copy.deepcopy(cache.loaded_segments), lens)
-    groups = []  # per layer: (kv, qheads)
-    for l in range(L):
-        by_kv = {}
-        for qh in cache.config.get_layer_class_a(l):
-            by_kv.setdefault(qh // G, []).append(qh)
-        groups.append(sorted(by_kv.items(), key=lambda x: x[0]))
-    audio_rel = [(a, e) for a, e in AUDIO]  # no left padding
-    offs = np.concatenate([[0], np.cumsum([e - a for a, e in AUDIO])])
+    sim = DecodeSimulation(cache, AUDIO)  # no left padding: audio relative to the segments' starts
     scale = D ** -0.5
-    plan = None
-    n_plans = 0
-    want_events = [[] for _ in range(B)]  # (step, c2g_tokens) of the decode-time loads
     for t in range(STEPS):
         qs = [torch.randn(B, HQ, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
         ks = [torch.randn(B, H, 1, D, generator=gen, device=dev).to(torch.bfloat16) for _ in range(L)]
@@ -154,58 +95,10 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monk
         outs = [decode_attention(cache, l, qs[l], ks[l], vs[l], scale, fused=fused) for l in range(L)]
         torch.cuda.synchronize()
         assert _lib.device_error() == 0, f"step {t}"
-        # the plan made from the previous step's scores applies now
-        if t > 0:
-            assert_topk_matches_oracle(cache.rec_topk[t - 1], cache.rec_acc[t - 1], offs,
-                                       cache._chunk_token_bounds, cache.config.top_k_chunks, f"step {t - 1}")
-            o.seq_lens = [list(x) for x in lens]
-            plan = o.step(cache.rec_topk[t - 1])
-            n_plans += int(plan.any_change)
-            for b in range(B):
-                n = sum(plan.load_lens[l][f] for l in range(L) for f in range(b * H, (b + 1) * H)) \
-                    if plan.any_change else 0
-                if n:
-                    want_events[b].append((t + 1, n))  # planned at step t, flushed with step t + 1
-            loaded_at_snapshot = [set(x) for x in o.loaded]
-        acc = np.zeros(int(offs[-1]))
-        for l in range(L):
-            nk = _bits(ks[l].reshape(B * H, D))
-            nv = _bits(vs[l].reshape(B * H, D))
-            cu_old = np.array(op.cu_from_lens(lens[l]), np.int32)
-            if plan is not None and plan.any_change:
-                load_k = np.concatenate([host_k[s:e] for s, e in plan.cpu_ranges]) if plan.cpu_ranges else \
-                    np.zeros((0, D), np.uint16)
-                load_v = np.concatenate([host_v[s:e] for s, e in plan.cpu_ranges]) if plan.cpu_ranges else \
-                    np.zeros((0, D), np.uint16)
-                cu_new = np.array(plan.cu_new[l], np.int32)
-                K[l], V[l] = oracle.rebuild_append_kv(
-                    K[l], V[l], nk, nv, load_k, load_v, cu_old, cu_new, plan.load_starts[l], plan.load_lens[l],
-                    plan.evict_offsets[l], plan.evict_starts[l], plan.evict_ends[l], plan.evict_max[l],
-                    dtype=oracle.DT_BF16)
-                lens[l] = list(plan.new_lens[l])
-            else:
-                cu_new = cu_old + np.arange(B * H + 1, dtype=np.int32)
-                K[l] = oracle.interleave_append(K[l], nk, cu_old, cu_new, dtype=oracle.DT_BF16)
-                V[l] = oracle.interleave_append(V[l], nv, cu_old, cu_new, dtype=oracle.DT_BF16)
-                lens[l] = [x + 1 for x in lens[l]]
-            dk, dv = cache.dense_kv(l)
-            np.testing.assert_array_equal(_bits(dk), K[l], err_msg=f"K step {t} layer {l}")
-            np.testing.assert_array_equal(_bits(dv), V[l], err_msg=f"V step {t} layer {l}")
-            cu = np.array(op.cu_from_lens(lens[l]), np.int32)
-            np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu)
-            q_flat = _bits(qs[l].reshape(B * H, G, D))
-            ref = oracle.decode_attn(q_flat, K[l], V[l], cu, scale, dtype=oracle.DT_BF16)
-            got = oracle.to_f64(_bits(outs[l].reshape(B * H, G, D)), oracle.DT_BF16)
-            ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
-            assert ok, f"attention step {t} layer {l}: {msg}"
-            qfull = _bits(qs[l].reshape(B, HQ, D))
-            for kv, qheads in groups[l]:
-                segs = [b * H + kv for b in range(B)]
-                oracle.segment_scores(qfull[:, qheads], K[l], [cu[s] for s in segs], [cu[s + 1] for s in segs],
-                                      [a for a, _ in audio_rel], [e for _, e in audio_rel], offs[:-1], scale, acc,
-                                      dtype=oracle.DT_BF16)
-        ok, msg = allclose_report(cache.rec_acc[t], acc, 1e-6, 1e-3)
-        assert ok, f"scores step {t}: {msg}"
+        sim.step(t, qs, ks, vs, outs)
+    lens, meta, host_k = sim.lens, sim.meta, sim.host_k
+    loaded_at_snapshot, want_events, loaded_after_prefill = sim.loaded_at_snapshot, sim.want_events, \
+        sim.loaded_after_prefill
     # the stats record (reference cache.py:1013-1081 and inference_stats.py):
     # the last snapshot is taken before the last step's plan
     stats = cache.get_all_stats()
@@ -231,11 +124,10 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monk
             assert got == want_events[b]
             assert all(e[3] == e[1] * row and e[2] == 0 for e in events[1:])
     if variant != "wnw_cpp":  # the deferred variant plans at the next step's start
-        o.seq_lens = [list(x) for x in lens]
-        o.step(cache.rec_topk[STEPS - 1])
+        sim.final_plan(STEPS - 1)
     for b in range(B):
-        assert set(cache._planner.get_loaded_segments(b)) == o.loaded[b]
-    assert n_plans > 0, "no compaction happened: the test would be vacuous"
+        assert set(cache._planner.get_loaded_segments(b)) == sim.planner.loaded[b]
+    assert sim.n_plans > 0, "no compaction happened: the test would be vacuous"
     counts = cache.layout_counts
     if layout == "slack":  # plans relocate changed segments until the tail is used up
         assert counts["relocate"] > 0 and counts["relayout"] == L, counts
