@@ -370,6 +370,27 @@ int wnw_fused_score_accumulate(const void* q, const void* k,
                                void* workspace, int64_t workspace_bytes,
                                void* stream);
 
+/*
+ * Chunk scores and the top-k chunk choice of the decode planner, one launch
+ * for every sample: the chunk selection of src/algorithms/wnw/code/
+ * cache.py:632-649 (prefix-sum chunk means, topk) in the batched form of
+ * src/algorithms/wnw_cpp/code/cache.py:160-171 (-1 where a sample has fewer
+ * chunks than k).  Sample b's scores are score_acc[score_offsets[b] ..
+ * score_offsets[b+1]); its chunks are entries chunk_offsets[b] ..
+ * chunk_offsets[b+1] of chunk_starts / chunk_ends (token bounds relative to
+ * the sample's first score).  A chunk's score is the mean of its scores
+ * (float32 sum / max(1, length)).  out_idx [n_samples, k]
+ * receives each sample's k best chunks in descending order of score, equal
+ * scores to the lower chunk index, -1 past the sample's chunk count.  At most
+ * 8192 chunks per sample and k <= 64; bounds outside the scores set
+ * WNW_DEVERR_BOUNDS (that chunk is never chosen).
+ */
+int wnw_chunk_topk(const float* score_acc, int64_t acc_len,
+                   const int32_t* score_offsets, int64_t n_samples,
+                   const int32_t* chunk_offsets, const int32_t* chunk_starts,
+                   const int32_t* chunk_ends, int64_t n_chunks, int64_t k,
+                   int32_t* out_idx, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Host planner (CPU only; no HIP calls)                                     */
 /* ------------------------------------------------------------------------ */

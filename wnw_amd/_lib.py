@@ -18,6 +18,7 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 ATTN_AUTO, ATTN_MFMA, ATTN_VALU, ATTN_STREAM = 0, 1, 2, 3
 DEVERR_BOUNDS, DEVERR_ORDER, DEVERR_CAPACITY = 1, 2, 4
 NOALLOC_SCRATCH_BYTES, NOALLOC_MAX_SEG = 16 << 20, 4096
+TOPK_MAX_CHUNKS, TOPK_MAX_K = 8192, 64  # wnw_chunk_topk: chunks of one sample, k
 
 _TORCH_DTYPES = {torch.float32: DT_F32, torch.float16: DT_F16, torch.bfloat16: DT_BF16}
 
@@ -52,6 +53,7 @@ _SIGNATURES = {
                                      _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp]),
     "wnw_fused_score_workspace_bytes": (_i64, [_i64, _i64]),
     "wnw_fused_score_accumulate": (_i32, [_vp] * 8 + [_i64] * 6 + [_f32, _i32, _vp, _i64, _vp]),
+    "wnw_chunk_topk": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     # host planner (CPU only)
     "wnw_planner_create": (_vp, [_i32, _i32, _i32, _i32]),
     "wnw_planner_destroy": (None, [_vp]),

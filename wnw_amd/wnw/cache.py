@@ -66,7 +66,8 @@ from ..kv.fused_attn import decode_attn, q1_decode_attn, q1_decode_attn_score
 from ..kv.kernels import append_inplace, interleave_append
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
-from .kernels import compact_segments, fused_score_accumulate, gather_host_rows, host_rows_readable, rebuild_append_kv
+from .kernels import (chunk_topk, compact_segments, fused_score_accumulate, gather_host_rows, host_rows_readable,
+                      rebuild_append_kv)
 
 
 @dataclass
@@ -384,17 +385,19 @@ class WnWCache(FlatVarlenCache):
         return {si for c in topk_chunks for si in self.chunk_to_segs[b][c]} - self.loaded_segments[b]
 
     def _topk_of(self, b: int, scores: Tensor) -> list[int]:
-        """cache.py:632-649: mean score per chunk (prefix sums), top-k."""
+        """cache.py:632-649: mean score per chunk, top-k (``wnw_chunk_topk``
+        over one sample)."""
         bounds = self._chunk_token_bounds[b]
         k = min(self.config.top_k_chunks, len(bounds))
         if k == 0:
             return []
-        prefix = torch.zeros(scores.shape[0] + 1, dtype=torch.float32, device=scores.device)
-        torch.cumsum(scores.float(), dim=0, out=prefix[1:])
-        st = torch.tensor([s for s, _ in bounds], dtype=torch.int64, device=scores.device)
-        en = torch.tensor([e for _, e in bounds], dtype=torch.int64, device=scores.device)
-        means = (prefix[en] - prefix[st]) / (en - st).clamp(min=1).float()
-        return means.topk(k).indices.tolist()
+        dev = scores.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        out = torch.empty(1, k, **i32)
+        chunk_topk(scores.float().contiguous(), torch.tensor([0, scores.shape[0]], **i32),
+                   torch.tensor([0, len(bounds)], **i32), torch.tensor([s for s, _ in bounds], **i32),
+                   torch.tensor([e for _, e in bounds], **i32), k, out)
+        return [c for c in out[0].tolist() if c >= 0]
 
     def _load_segments_for_sample(self, b: int, segs: set[int]) -> None:
         """cache.py:651-714: append the host rows of `segs` to every class-B
@@ -599,30 +602,28 @@ class WnWCache(FlatVarlenCache):
                 self._ca_kv_mask_by_layer.append(None)
         self._decode_audio_starts_b = torch.tensor(self._audio_starts_list, dtype=torch.int32, device=self.device)
         self._decode_audio_ends_b = torch.tensor(self._audio_ends_list, dtype=torch.int32, device=self.device)
-        # chunk scoring on the device: padded [B, W] prefix sums of the accumulator
+        # chunk scoring on the device (one launch of wnw_chunk_topk): every
+        # sample's chunks as a CSR of token bounds relative to its scores
         B = self.batch_size
-        W = self._max_audio + 1
-        scatter, gk_s, gk_e, gk_len, gk_pos = [], [], [], [], []
-        self._max_chunks = max((len(c) for c in self.chunk_to_segs), default=0)
-        for b in range(B):
-            base = b * W
-            n = self._score_offsets_list[b + 1] - self._score_offsets_list[b]
-            scatter += range(base + 1, base + 1 + n)
-            for c, (s, e) in enumerate(self._chunk_token_bounds[b]):
-                gk_s.append(base + s)
-                gk_e.append(base + e)
-                gk_len.append(max(1, e - s))
-                gk_pos.append(b * self._max_chunks + c)
         dev = self.device
-        self._tk_scatter = torch.tensor(scatter, dtype=torch.int64, device=dev)
-        self._tk_s = torch.tensor(gk_s, dtype=torch.int64, device=dev)
-        self._tk_e = torch.tensor(gk_e, dtype=torch.int64, device=dev)
-        self._tk_len = torch.tensor(gk_len, dtype=torch.float32, device=dev)
-        self._tk_pos = torch.tensor(gk_pos, dtype=torch.int64, device=dev)
-        self._tk_padded = torch.zeros(B, W, dtype=torch.float32, device=dev)
-        self._tk_prefix = torch.empty(B, W, dtype=torch.float32, device=dev)
-        self._tk_grid = torch.full((B * max(1, self._max_chunks),), float("-inf"), dtype=torch.float32, device=dev)
+        self._max_chunks = max((len(c) for c in self.chunk_to_segs), default=0)
+        if self._max_chunks > _lib.TOPK_MAX_CHUNKS:
+            raise ValueError(f"{self._max_chunks} chunks in one sample; the device top-k takes at most "
+                             f"{_lib.TOPK_MAX_CHUNKS}")
         self._tk_k = min(self.config.top_k_chunks, self._max_chunks)
+        if self._tk_k > _lib.TOPK_MAX_K:
+            raise ValueError(f"top_k_chunks {self._tk_k} above the device top-k's {_lib.TOPK_MAX_K}")
+        bounds = [se for b in range(B) for se in self._chunk_token_bounds[b]]
+        self._tk_chunk_off = torch.tensor([0] + list(accumulate(len(self._chunk_token_bounds[b]) for b in range(B))),
+                                          dtype=torch.int32, device=dev)
+        self._tk_s = torch.tensor([s for s, _ in bounds], dtype=torch.int32, device=dev)
+        self._tk_e = torch.tensor([e for _, e in bounds], dtype=torch.int32, device=dev)
+        k = max(1, self._tk_k)
+        self._tk_out = torch.empty(B, k, dtype=torch.int32, device=dev)
+        # the choice comes back through pinned memory and an event: the host
+        # waits for the top-k launch only, not for the device to go idle
+        self._tk_host = torch.empty(B, k, dtype=torch.int32, pin_memory=True)
+        self._tk_event = torch.cuda.Event()
 
     # ----------------------------------------------------------------- decode
     def _before_decode_layer(self, layer_idx: int) -> None:
@@ -851,26 +852,29 @@ class WnWCache(FlatVarlenCache):
         self.score_accumulator.zero_()
 
     # ---------------------------------------------------------------- planning
-    def _topk_scores_async(self) -> Tensor | None:
+    def _topk_scores_async(self):
         """Top-k chunks of every sample from the accumulator, on the device
-        (src/algorithms/wnw_cpp/code/cache.py:160-171): chunk means from
-        padded prefix sums, -1 where a sample has fewer chunks than k."""
+        (src/algorithms/wnw_cpp/code/cache.py:160-171): one launch of
+        ``wnw_chunk_topk`` (chunk means, k best per sample, -1 where a sample
+        has fewer chunks than k), then a copy of the [B, k] choice into pinned
+        memory and an event behind it.  Nothing waits here; the handle goes
+        to ``_topk_finalize``."""
         if self._tk_k == 0:
             return None
-        self._tk_padded.view(-1).index_copy_(0, self._tk_scatter, self.score_accumulator)
-        torch.cumsum(self._tk_padded, dim=1, out=self._tk_prefix)
-        pf = self._tk_prefix.view(-1)
-        self._tk_grid.index_copy_(0, self._tk_pos, (pf[self._tk_e] - pf[self._tk_s]) / self._tk_len)
-        vals, idx = self._tk_grid.view(self.batch_size, self._max_chunks).topk(self._tk_k, dim=1)
-        idx = idx.to(torch.int32)
-        return torch.where(vals > float("-inf"), idx, torch.full_like(idx, -1))
+        chunk_topk(self.score_accumulator, self.score_offsets, self._tk_chunk_off, self._tk_s, self._tk_e,
+                   self._tk_k, self._tk_out)
+        self._tk_host.copy_(self._tk_out, non_blocking=True)
+        self._tk_event.record()
+        return self._tk_host
 
-    def _topk_finalize(self, idx_masked: Tensor | None) -> tuple[Tensor, Tensor]:
-        """CSR of the chosen chunks per sample (wnw_cpp/code/cache.py:173-189)."""
-        if idx_masked is None:
+    def _topk_finalize(self, pending) -> tuple[Tensor, Tensor]:
+        """CSR of the chosen chunks per sample (wnw_cpp/code/cache.py:173-189),
+        after waiting for the top-k's event (the launch and its copy only)."""
+        if pending is None:
             return torch.empty(0, dtype=torch.int32), torch.zeros(self.batch_size + 1, dtype=torch.int32)
+        self._tk_event.synchronize()
         flat, off = [], [0]
-        for row in idx_masked.tolist():
+        for row in pending.tolist():
             flat += [c for c in row if c >= 0]
             off.append(len(flat))
         return torch.tensor(flat, dtype=torch.int32), torch.tensor(off, dtype=torch.int32)

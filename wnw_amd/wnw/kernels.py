@@ -192,6 +192,35 @@ def compact_segments(
         "compact_segments")
 
 
+def chunk_topk(score_acc: torch.Tensor, score_offsets: torch.Tensor, chunk_offsets: torch.Tensor,
+               chunk_starts: torch.Tensor, chunk_ends: torch.Tensor, k: int, out: torch.Tensor) -> torch.Tensor:
+    """Each sample's k best chunks by mean score, into ``out`` (int32
+    [B, k], -1 past the sample's chunk count), in one launch (``wnw_chunk_topk``).
+
+    The chunk selection of the reference (src/algorithms/wnw/code/
+    cache.py:632-649; batched, src/algorithms/wnw_cpp/code/cache.py:160-171).
+    ``score_offsets`` [B + 1] bounds each sample's scores in ``score_acc``;
+    ``chunk_offsets`` [B + 1] each sample's chunks in ``chunk_starts`` /
+    ``chunk_ends`` (token bounds relative to the sample's first score).
+    Equal means go to the lower chunk index."""
+    _lib.require_gpu(score_acc, score_offsets, chunk_offsets, chunk_starts, chunk_ends, out)
+    B = score_offsets.numel() - 1
+    for name, t in (("score_offsets", score_offsets), ("chunk_offsets", chunk_offsets),
+                    ("chunk_starts", chunk_starts), ("chunk_ends", chunk_ends), ("out", out)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise _lib.WnwError(f"{name} must be a contiguous int32 tensor")
+    if score_acc.dtype != torch.float32 or not score_acc.is_contiguous():
+        raise _lib.WnwError("score_acc must be a contiguous float32 tensor")
+    if chunk_offsets.numel() != B + 1 or out.shape != (B, k) or chunk_starts.numel() != chunk_ends.numel():
+        raise _lib.WnwError("chunk_offsets must be [B + 1], out [B, k], chunk_starts / chunk_ends equal")
+    _lib.ensure_init(score_acc.device)
+    _lib.check(_lib.lib().wnw_chunk_topk(
+        _lib.ptr(score_acc), score_acc.numel(), _lib.ptr(score_offsets), B, _lib.ptr(chunk_offsets),
+        _lib.ptr(chunk_starts), _lib.ptr(chunk_ends), chunk_starts.numel(), int(k), _lib.ptr(out),
+        _lib.stream_of(score_acc.device)), "chunk_topk")
+    return out
+
+
 def host_rows_readable(host_k: torch.Tensor, host_v: torch.Tensor) -> bool:
     """Whether the device can read the two host arrays directly (pinned)."""
     return bool(_lib.lib().wnw_host_rows_readable(_lib.ptr(host_k), _lib.ptr(host_v)))
