@@ -1002,13 +1002,15 @@ template <typename T, int D, int NW, int QD, bool XL, bool APPEND>
 // are addressed without a kernel-argument load; aggregates are not preloaded.
 __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_arg, const void* k_arg, const void* v_arg,
                                                                const int32_t* cu_arg, const int64_t* base_arg,
-                                                               uint64_t inv_arg, int32_t nseg_arg, int32_t g_arg,
+                                                               const int32_t* cap_arg, uint64_t inv_arg,
+                                                               int32_t nseg_arg, int32_t g_arg,
                                                                AttnParams p) {
   p.q = q_arg;
   p.k = k_arg;
   p.v = v_arg;
   p.cu = cu_arg;
   p.base = base_arg;
+  p.cap = cap_arg;
   p.split_inv = inv_arg;
   p.n_seg = nseg_arg;
   p.G = g_arg;
@@ -1940,7 +1942,7 @@ static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t 
                          stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND));
   if (attr_err != hipSuccess) return attr_err;
   hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
-                     st, ap.q, ap.k, ap.v, ap.cu, ap.base, ap.split_inv, ap.n_seg, ap.G, ap);
+                     st, ap.q, ap.k, ap.v, ap.cu, ap.base, ap.cap, ap.split_inv, ap.n_seg, ap.G, ap);
   return hipGetLastError();
 }
 
