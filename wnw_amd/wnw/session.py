@@ -67,6 +67,43 @@ def decode_attention(cache, layer_idx: int, q: Tensor, k: Tensor, v: Tensor, sca
     return out
 
 
+def prefill_attention(q: Tensor, k: Tensor, v: Tensor, attention_mask: Tensor | None, scaling: float,
+                      q_chunk: int = 1024) -> Tensor:
+    """Prompt attention of the prefill branch (session.py:53-63: SDPA with
+    the model's mask, causal when there is none).  q/k/v: [B, Hq, S, D]
+    (K/V already repeated over the group).
+
+    SDPA runs with its fused backends only (flash, memory-efficient); when
+    neither takes the inputs, the same attention is computed in float32
+    over query chunks with contiguous operands (the products in float32,
+    so no batched bf16 product with a transposed operand is issued)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, attn_mask=attention_mask, scale=scaling,
+                                                  is_causal=attention_mask is None)
+    except RuntimeError:
+        pass
+    B, Hq, S, D = q.shape
+    Skv = k.shape[2]
+    kt = k.float().transpose(-1, -2).contiguous()
+    vf = v.float().contiguous()
+    if attention_mask is not None and attention_mask.dtype == torch.bool:
+        attention_mask = torch.where(attention_mask, 0.0, float("-inf"))
+    out = torch.empty(B, Hq, S, D, dtype=q.dtype, device=q.device)
+    for i0 in range(0, S, q_chunk):
+        i1 = min(S, i0 + q_chunk)
+        s = torch.matmul(q[:, :, i0:i1].float().contiguous(), kt) * scaling
+        if attention_mask is None:
+            rows = torch.arange(i0, i1, device=q.device).unsqueeze(1) + (Skv - S)
+            s = s.masked_fill(torch.arange(Skv, device=q.device).unsqueeze(0) > rows, float("-inf"))
+        else:
+            s = s + attention_mask[..., i0:i1, :].float()
+        out[:, :, i0:i1] = torch.matmul(s.softmax(dim=-1), vf).to(q.dtype)
+    return out
+
+
 def compute_prefill_scores(q: Tensor, k: Tensor, attention_mask: Tensor | None, cache, layer_idx: int,
                            num_kv_heads: int, num_kv_groups: int, scaling: float):
     """Prefill token scores (session.py:119-169): class-A scores from the
@@ -173,9 +210,8 @@ class WnWSession(AlgorithmSession):
             if not cache.prefilled:
                 cache.prefill_before_attn(layer_idx)
                 cache.update(k, v, layer_idx)
-                out = F.scaled_dot_product_attention(q, k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1),
-                                                     attn_mask=attention_mask, scale=scaling,
-                                                     is_causal=attention_mask is None)
+                out = prefill_attention(q, k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1),
+                                        attention_mask, scaling)
                 ca, per_head = compute_prefill_scores(q, k, attention_mask, cache, layer_idx, H, G, scaling)
                 cache.prefill_after_attn(layer_idx, ca, per_head, k, v)
                 if last:
