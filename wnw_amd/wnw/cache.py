@@ -93,8 +93,22 @@ def _compute_chunks(segments: list[tuple[int, int]], chunk_size: int, stride: in
     return [list(range(i, min(i + per, n))) for i in range(n)]
 
 
+def _to_device(data, dtype: torch.dtype, device: torch.device) -> Tensor:
+    """A host list or CPU tensor on the device without waiting for the
+    device: staged in a fresh pinned block and copied asynchronously on the
+    current stream (the host allocator reuses the block only after the copy
+    is done, and the caller's CPU tensor may be overwritten at once).  A
+    pageable host->device copy would wait for the stream's earlier work."""
+    t = data if isinstance(data, Tensor) else torch.tensor(data, dtype=dtype)
+    if torch.device(device).type == "cpu":
+        return t.to(dtype, copy=True)
+    staged = torch.empty(t.shape, dtype=dtype, pin_memory=True)
+    staged.copy_(t)
+    return staged.to(device, non_blocking=True)
+
+
 def _build_cu_seqlens(seq_lens: list[int], device: torch.device) -> Tensor:
-    return torch.tensor(_build_cu_seqlens_list(seq_lens), dtype=torch.int32, device=device)
+    return _to_device(_build_cu_seqlens_list(seq_lens), torch.int32, device)
 
 
 def _build_cu_seqlens_list(seq_lens: list[int]) -> list[int]:
@@ -147,12 +161,13 @@ class WnWCache(FlatVarlenCache):
         if slack_rows < 0:
             raise ValueError("slack_rows must be >= 0")
         self.slack_rows = int(slack_rows)
-        # free tail of a pool with host rows: max(tail_rows_min, tail_factor x
-        # the class-B rows), the room for segments a plan relocates
+        # flip region of a pool with host rows: two halves of max(tail_rows_min,
+        # tail_factor x the class-B rows) each; a plan moves the layer's
+        # class-B segments into the half they do not occupy
         self.tail_rows_min = 1024
         self.tail_factor = 2
         # layout changes so far: (fresh pools, fresh pools applying a plan,
-        # plans applied by relocating segments into the tail)
+        # plans applied by moving the class-B segments to the other half)
         self.layout_counts = {"relayout": 0, "relayout_plan": 0, "relocate": 0}
         if config.num_layers == 0:
             config.set_model_dims(num_layers, num_kv_heads, num_q_heads)
@@ -246,7 +261,11 @@ class WnWCache(FlatVarlenCache):
         self._cap_list: list[list[int] | None] = [None] * L
         self._cu_spare: list[Tensor | None] = [None] * L  # the offsets buffer the next append writes
         self._headroom = [0] * L                          # min over segments of cap - len
-        self._tail = [0] * L                              # first free row after the segments
+        self._half_start = [0] * L                        # first row of the flip region
+        self._half_size = [0] * L                         # rows of each of its two halves
+        self._flip = [0] * L                              # the half the next plan moves into
+        self._moves: list = [None] * L                    # a pending plan's layout per layer
+        self._move_dev = None                             # ... and its device arrays
         self._max_len = [0] * L
         self._rows = [0] * L                              # sum of the segment lengths
 
@@ -441,16 +460,20 @@ class WnWCache(FlatVarlenCache):
         self._zeros_n = torch.zeros(N, dtype=torch.int32, device=self.device)
         self._zeros_n1 = torch.zeros(N + 1, dtype=torch.int32, device=self.device)
         self._empty_i32 = torch.empty(0, dtype=torch.int32, device=self.device)
+        H = self.num_kv_heads
+        self._classb_segs = [[f for f in range(N) if f % H in set(self._class_b_heads_by_layer[l])]
+                             for l in range(self.num_layers)]
+        self._classb_segs_dev = [torch.tensor(x, dtype=torch.int32, device=self.device) for x in self._classb_segs]
         for l in range(self.num_layers):
             self._rows[l] = sum(self.seq_lens[l])
             self._max_len[l] = max(self.seq_lens[l], default=0)
             if self.slack_layout:
                 self._relayout(l)
 
-    def _tail_rows(self, layer_idx: int, lens: list[int]) -> int:
-        """Free rows kept after the segments, for segments a plan changes
-        (relocated there with their slack): ``tail_factor`` times the room
-        the layer's class-B segments take, at least ``tail_rows_min``, when
+    def _half_rows(self, layer_idx: int, lens: list[int]) -> int:
+        """Rows of each half of the flip region after the segments, where
+        plans put the class-B segments (with their slack): ``tail_factor``
+        times the room those segments take, at least ``tail_rows_min``, when
         there are host rows to load, else none (no plan changes a layout
         without them)."""
         if self.cpu_restore_k is None or self.cpu_restore_k.shape[0] == 0:
@@ -473,12 +496,13 @@ class WnWCache(FlatVarlenCache):
         caps = [_round8(n + self.slack_rows) for n in new_lens]
         bases = [0] + list(accumulate(caps))[:-1]
         used = sum(caps)
-        pool = used + self._tail_rows(l, new_lens)
+        half = self._half_rows(l, new_lens)
+        pool = used + 2 * half
         cu = self.cu_seqlens_k[l]
         src_base = self.seg_base[l] if self.seg_base[l] is not None else cu[:-1].to(torch.int64)
         src_len = cu[1:] - cu[:-1]
-        dst_base = torch.tensor(bases, dtype=torch.int64, device=dev)
-        new_len_t = torch.tensor(new_lens, dtype=torch.int32, device=dev)
+        dst_base = _to_device(bases, torch.int64, dev)
+        new_len_t = _to_device(new_lens, torch.int32, dev)
         old_k, old_v = self.layer_k[l], self.layer_v[l]
         k = torch.empty(pool, D, dtype=old_k.dtype, device=dev)
         v = torch.empty_like(k)
@@ -493,19 +517,22 @@ class WnWCache(FlatVarlenCache):
                                  plan["evict_offsets"], plan["evict_starts"], plan["evict_ends"], max(new_lens))
         self.layer_k[l], self.layer_v[l] = k, v
         self.seg_base[l] = dst_base
-        self.seg_cap[l] = torch.tensor(caps, dtype=torch.int32, device=dev)
+        self.seg_cap[l] = _to_device(caps, torch.int32, dev)
         self._base_list[l], self._cap_list[l] = bases, caps
-        self._tail[l] = used
+        self._half_start[l], self._half_size[l], self._flip[l] = used, half, 0
         self._set_lens(l, new_lens)
         self.layout_counts["relayout" if plan is None else "relayout_plan"] += 1
 
-    def _set_lens(self, layer_idx: int, lens: list[int]) -> None:
-        """Host lengths and device offsets of a layer after a layout change."""
+    def _set_lens(self, layer_idx: int, lens: list[int], cu_dev: Tensor | None = None) -> None:
+        """Host lengths and device offsets of a layer after a layout change
+        (``cu_dev``: the offsets already on the device)."""
         l = layer_idx
         self.seq_lens[l] = list(lens)
         self.cu_seqlens_list[l] = _build_cu_seqlens_list(self.seq_lens[l])
-        self.cu_seqlens_k[l] = torch.tensor(self.cu_seqlens_list[l], dtype=torch.int32, device=self.device)
-        self._cu_spare[l] = torch.empty_like(self.cu_seqlens_k[l])
+        self.cu_seqlens_k[l] = cu_dev if cu_dev is not None else \
+            _to_device(self.cu_seqlens_list[l], torch.int32, self.device)
+        if self._cu_spare[l] is None or self._cu_spare[l].shape != self.cu_seqlens_k[l].shape:
+            self._cu_spare[l] = torch.empty_like(self.cu_seqlens_k[l])
         self._rows[l] = self.cu_seqlens_list[l][-1]
         self._max_len[l] = max(lens, default=0)
         self._headroom[l] = min((c - n for c, n in zip(self._cap_list[l], lens)), default=0)
@@ -755,57 +782,78 @@ class WnWCache(FlatVarlenCache):
             self._relayout(layer_idx)
 
     def _apply_pending_slack(self, layer_idx: int) -> None:
-        """A pending plan's compaction + loads for this layer (slack layout):
-        the segments the plan changes are rebuilt into the pool's free tail
-        (their old rows are left behind), or, when the tail is used up, the
+        """A pending plan's compaction + loads for this layer (slack layout),
+        as decided when the plan was made (``_plan_slack_moves``): the
+        class-B segments move into the free half of the flip region, or the
         whole layer into a fresh pool.  Lengths and offsets become the
         plan's, without the step's append (the append follows)."""
         l = layer_idx
         if not self._pending_chunk_update or self._pending_cu_new[l] is None:
             return
         self._wait_loads(l)
-        o = self._plan_out
-        ll, eo = o["load_lens_2d"][l], o["evict_offsets_2d"][l]
-        new_lens = [x - 1 for x in self._pending_new_lens[l]]  # the append comes next
-        changed = ((ll > 0) | (eo[1:] > eo[:-1])).nonzero().flatten().tolist()
-        if changed:
-            need = sum(_round8(new_lens[s] + self.slack_rows) for s in changed)
-            plan = dict(lens=new_lens, load_k=self._pending_gpu_k, load_v=self._pending_gpu_v,
-                        load_starts=self._pending_load_starts[l], load_lens=self._pending_load_lens[l],
-                        evict_offsets=self._pending_evict_offsets[l], evict_starts=self._pending_evict_starts[l],
-                        evict_ends=self._pending_evict_ends[l])
-            if self._tail[l] + need <= self.layer_k[l].shape[0]:
-                self._relocate(l, changed, plan)
-            else:
-                self._relayout(l, plan)
-        else:
-            self._set_lens(l, new_lens)
+        kind, bases, caps, lens = self._moves[l]
+        if kind == "relayout":
+            self._relayout(l, dict(lens=lens, load_k=self._pending_gpu_k, load_v=self._pending_gpu_v,
+                                   load_starts=self._pending_load_starts[l], load_lens=self._pending_load_lens[l],
+                                   evict_offsets=self._pending_evict_offsets[l],
+                                   evict_starts=self._pending_evict_starts[l], evict_ends=self._pending_evict_ends[l]))
+        elif kind == "move":
+            self._move_class_b(l, bases, caps, lens)
+        self._moves[l] = None
         self._pending_layers_applied += 1
         if self._pending_layers_applied == self.num_layers:
             self._pending_chunk_update = False
             self._clear_pending_rebuild_state()
+            self._move_dev = None
 
-    def _relocate(self, layer_idx: int, changed: list[int], plan: dict) -> None:
-        """The changed segments, compacted with their loads, into fresh rows
-        of the pool's free tail (disjoint from every segment's rows)."""
-        l, dev = layer_idx, self.device
-        bases, caps = list(self._base_list[l]), list(self._cap_list[l])
-        t = self._tail[l]
-        for s in changed:
-            bases[s], caps[s] = t, _round8(plan["lens"][s] + self.slack_rows)
-            t += caps[s]
-        cu = self.cu_seqlens_k[l]
-        dst_base = torch.tensor(bases, dtype=torch.int64, device=dev)
+    def _plan_slack_moves(self, new_lens_all: list[list[int]]) -> None:
+        """Where a plan puts every layer's rows (slack layout), decided on the
+        host when the plan is made, with the device arrays sent in one copy
+        each for all layers.  In a layer the plan changes, every class-B
+        segment (changed or not) is compacted with its loads into the half
+        of the flip region the class-B segments do not occupy, packed with
+        their slack; so the half they leave is wholly free for the next plan
+        and no search for room is needed.  A layer whose block does not fit
+        a half gets a fresh pool instead (``_relayout`` with the plan)."""
+        o = self._plan_out
+        bases_all, caps_all, lens_all, src_all, cu_all = [], [], [], [], []
+        for l in range(self.num_layers):
+            ll, eo = o["load_lens_2d"][l], o["evict_offsets_2d"][l]
+            lens = [x - 1 for x in new_lens_all[l]]  # the step's append comes after the move
+            bases, caps = list(self._base_list[l]), list(self._cap_list[l])
+            kind = "none"
+            if bool(((ll > 0) | (eo[1:] > eo[:-1])).any()):
+                t0 = t = self._half_start[l] + self._flip[l] * self._half_size[l]
+                for f in self._classb_segs[l]:
+                    bases[f], caps[f] = t, _round8(lens[f] + self.slack_rows)
+                    t += caps[f]
+                kind = "move" if t - t0 <= self._half_size[l] else "relayout"
+            self._moves[l] = (kind, bases, caps, lens)
+            bases_all.append(bases)
+            caps_all.append(caps)
+            lens_all.append(lens)
+            src_all.append(self.seq_lens[l])
+            cu_all.append(_build_cu_seqlens_list(lens))
+        dev = self.device
+        self._move_dev = (_to_device(bases_all, torch.int64, dev), _to_device(caps_all, torch.int32, dev),
+                          _to_device(lens_all, torch.int32, dev), _to_device(src_all, torch.int32, dev),
+                          _to_device(cu_all, torch.int32, dev))
+
+    def _move_class_b(self, layer_idx: int, bases: list[int], caps: list[int], lens: list[int]) -> None:
+        """The layer's class-B segments, compacted with their loads, into the
+        free half of the flip region (disjoint from every segment's rows)."""
+        l = layer_idx
+        bdev, cdev, ldev, sdev, cudev = self._move_dev
         k, v = self.layer_k[l], self.layer_v[l]
-        compact_segments(k, v, k, v, torch.tensor(changed, dtype=torch.int32, device=dev), self.seg_base[l],
-                         cu[1:] - cu[:-1], dst_base, torch.tensor(plan["lens"], dtype=torch.int32, device=dev),
-                         plan["load_k"], plan["load_v"], plan["load_starts"], plan["load_lens"], plan["evict_offsets"],
-                         plan["evict_starts"], plan["evict_ends"], max(plan["lens"][s] for s in changed))
-        self.seg_base[l] = dst_base
-        self.seg_cap[l] = torch.tensor(caps, dtype=torch.int32, device=dev)
+        segs = self._classb_segs[l]
+        compact_segments(k, v, k, v, self._classb_segs_dev[l], self.seg_base[l], sdev[l], bdev[l], ldev[l],
+                         self._pending_gpu_k, self._pending_gpu_v, self._pending_load_starts[l],
+                         self._pending_load_lens[l], self._pending_evict_offsets[l], self._pending_evict_starts[l],
+                         self._pending_evict_ends[l], max(lens[f] for f in segs))
+        self.seg_base[l], self.seg_cap[l] = bdev[l], cdev[l]
         self._base_list[l], self._cap_list[l] = bases, caps
-        self._tail[l] = t
-        self._set_lens(l, plan["lens"])
+        self._flip[l] ^= 1
+        self._set_lens(l, lens, cu_dev=cudev[l])
         self.layout_counts["relocate"] += 1
 
     def decode_after_attn(self, layer_idx: int, q: Tensor) -> None:
@@ -906,10 +954,12 @@ class WnWCache(FlatVarlenCache):
         self._clear_pending_rebuild_state()
         o = self._plan_out
         dev = self.device
-        ls, ll, cun = (o["load_starts_2d"].to(dev), o["load_lens_2d"].to(dev), o["cu_new_2d"].to(dev))
-        eoff = o["evict_offsets_2d"].to(dev)
-        evs = ev_s.to(dev) if ev_s.numel() else self._empty_i32
-        eve = ev_e.to(dev) if ev_e.numel() else self._empty_i32
+        i32 = torch.int32
+        ls, ll, cun = (_to_device(o["load_starts_2d"], i32, dev), _to_device(o["load_lens_2d"], i32, dev),
+                       _to_device(o["cu_new_2d"], i32, dev))
+        eoff = _to_device(o["evict_offsets_2d"], i32, dev)
+        evs = _to_device(ev_s, i32, dev) if ev_s.numel() else self._empty_i32
+        eve = _to_device(ev_e, i32, dev) if ev_e.numel() else self._empty_i32
         elp, emax, new_lens = o["evict_layer_ptr"].tolist(), o["evict_max"].tolist(), o["new_lens_2d"].tolist()
         for l in range(self.num_layers):
             self._pending_load_starts[l], self._pending_load_lens[l], self._pending_cu_new[l] = ls[l], ll[l], cun[l]
@@ -920,6 +970,8 @@ class WnWCache(FlatVarlenCache):
             self._pending_evict_starts[l] = evs[lo:hi] if hi > lo else self._empty_i32
             self._pending_evict_ends[l] = eve[lo:hi] if hi > lo else self._empty_i32
         self._segments_changed_ranges = ranges
+        if self.slack_layout:
+            self._plan_slack_moves(new_lens)
         dt = self.layer_k[0].dtype
         if total > 0 and self._record_plan_transfers and self.stats.enabled:
             # cache.py:816-820: host rows loaded per sample (K and V)
@@ -966,8 +1018,8 @@ class WnWCache(FlatVarlenCache):
         events = [None] * self.num_layers
         per_launch = max(1, -(-self.num_layers // self._gather_launches))
         with torch.cuda.stream(stream):
-            rg = ranges.to(dev)
-            do = dst.to(dev)
+            rg = _to_device(ranges, ranges.dtype, dev)
+            do = _to_device(dst, dst.dtype, dev)
             pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
             pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
             r0 = 0
@@ -1131,7 +1183,7 @@ def _compact_no_append(cache: WnWCache, layer_idx: int, cu_mid: Tensor, lens_aft
     compact_segments(
         cache.layer_k[layer_idx], cache.layer_v[layer_idx], k, v, torch.arange(N, dtype=torch.int32, device=dev),
         cu_old[:-1].to(torch.int64), (cu_old[1:] - cu_old[:-1]).to(torch.int32), cu_mid[:-1].to(torch.int64),
-        torch.tensor(lens_after, dtype=torch.int32, device=dev), cache._pending_gpu_k, cache._pending_gpu_v,
+        _to_device(lens_after, torch.int32, dev), cache._pending_gpu_k, cache._pending_gpu_v,
         cache._pending_load_starts[layer_idx], cache._pending_load_lens[layer_idx],
         cache._pending_evict_offsets[layer_idx], cache._pending_evict_starts[layer_idx],
         cache._pending_evict_ends[layer_idx], max(lens_after) if lens_after else 0)
