@@ -391,6 +391,34 @@ int wnw_chunk_topk(const float* score_acc, int64_t acc_len,
                    const int32_t* chunk_ends, int64_t n_chunks, int64_t k,
                    int32_t* out_idx, void* stream);
 
+/*
+ * Host->device transfer engine for a plan's offloaded rows: the gather into
+ * pinned staging of src/algorithms/wnw_cpp/code/planner.cpp:113-122 and the
+ * side-stream copy + wait of src/algorithms/wnw/code/cache.py:716-721 and
+ * :868-881, run by a background thread with a pool of gather threads.  The
+ * ranges (host rows [ranges[2r], ranges[2r+1]) of host_k / host_v, in
+ * transfer order) are split into groups (ranges group_ranges[g] ..
+ * group_ranges[g+1]); group by group the rows are gathered into
+ * consecutive staging rows, copied (hipMemcpyAsync, the DMA engines) to the
+ * same rows of dev_k / dev_v on `stream`, and an event is recorded.
+ * wnw_h2d_start returns at once (after the previous start is fully issued);
+ * wnw_h2d_wait makes a stream wait for one group's copy (the host blocks
+ * only until that copy is issued); wnw_h2d_join waits until every group is
+ * issued.  Staging is used in two alternating pairs by the caller: a start
+ * waits for the copies of the start before the previous one (the last use
+ * of its pair) before gathering.  At most 64 groups.
+ */
+typedef struct wnw_h2d wnw_h2d;
+wnw_h2d* wnw_h2d_create(int n_workers);  /* NULL on error */
+void wnw_h2d_destroy(wnw_h2d* x);
+int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v,
+                  int64_t host_rows, const int32_t* ranges, int64_t n_ranges,
+                  const int64_t* group_ranges, int n_groups, void* stg_k,
+                  void* stg_v, int64_t stg_rows, void* dev_k, void* dev_v,
+                  int64_t dev_rows, int64_t row_bytes, void* stream);
+int wnw_h2d_wait(wnw_h2d* x, int group, void* stream);
+int wnw_h2d_join(wnw_h2d* x);
+
 /* ------------------------------------------------------------------------ */
 /* Host planner (CPU only; no HIP calls)                                     */
 /* ------------------------------------------------------------------------ */

@@ -62,13 +62,14 @@ LAYOUTS = {"slack": dict(slack_rows=256), "tight": dict(slack_rows=3, tail=0), "
 
 
 @pytest.mark.parametrize("layout", ["slack", "tight", "dense"])
-@pytest.mark.parametrize("variant,fused,host_gather", [("wnw", True, False), ("wnw", False, False),
-                                                       ("wnw_fallback", True, False), ("wnw_cpp", True, False),
-                                                       ("wnw", True, True), ("wnw_cpp", True, True)])
-def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monkeypatch):
+@pytest.mark.parametrize("variant,fused,offload", [("wnw", True, "copy"), ("wnw", False, "copy"),
+                                                   ("wnw_fallback", True, "copy"), ("wnw_cpp", True, "copy"),
+                                                   ("wnw", True, "device"), ("wnw_cpp", True, "device")])
+def test_decode_steps_match_simulation(variant, fused, offload, layout, monkeypatch):
     dev = torch.device("cuda", 0)
-    if host_gather:  # loads through the host gather + staging copy instead of the device gather
-        monkeypatch.setenv("WNW_HOST_GATHER", "1")
+    # loads through the transfer engine (host gather threads + DMA copies) or
+    # the device gather kernel reading pinned memory
+    monkeypatch.setenv("WNW_OFFLOAD", offload)
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     cls = _recording(WnWCppCache if variant == "wnw_cpp" else WnWCache)
@@ -80,11 +81,11 @@ def test_decode_steps_match_simulation(variant, fused, host_gather, layout, monk
     if variant == "wnw_fallback":
         cache.use_triton_rebuild = False
     cache.collect_stats(1)  # a snapshot every decode step
-    print(f"cache variant={variant} fused={fused} host_gather={host_gather} layout={layout}", flush=True)
+    print(f"cache variant={variant} fused={fused} offload={offload} layout={layout}", flush=True)
     _prefill(cache, dev, gen)
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
-    assert cache._device_gather == (not host_gather)
+    assert cache._offload == offload
 
     sim = DecodeSimulation(cache, AUDIO)  # no left padding: audio relative to the segments' starts
     scale = D ** -0.5

@@ -51,11 +51,12 @@ def _config():
                      prefill_score_mode="last", num_layers=L, num_kv_heads=HKV, num_q_heads=HQ)
 
 
-@pytest.mark.parametrize("fused,host_gather", [(True, False), (False, False), (True, True)])
-def test_cfg4_decode_steps_match_simulation(fused, host_gather, monkeypatch):
+@pytest.mark.parametrize("fused,offload", [(True, "copy"), (False, "copy"), (True, "device")])
+def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
     dev = torch.device("cuda", 0)
-    if host_gather:  # the reference's host gather into pinned staging + copy
-        monkeypatch.setenv("WNW_HOST_GATHER", "1")
+    # the transfer engine (host gather threads + DMA copies per group of
+    # layers) or the device gather kernel reading pinned memory
+    monkeypatch.setenv("WNW_OFFLOAD", offload)
     cfg = _config()
     cache = recording(WnWCache)(cfg, L, HKV, HQ, D, dev)
     cache.rec_acc, cache.rec_topk = [], []
@@ -64,7 +65,7 @@ def test_cfg4_decode_steps_match_simulation(fused, host_gather, monkeypatch):
     cache.setup_audio(torch.tensor([TEXT], device=dev), torch.tensor([TEXT + AUDIO], device=dev), None)
     gen = torch.Generator(device=dev)
     gen.manual_seed(11)
-    print(f"cfg4 cache test fused={fused} host_gather={host_gather}: prefill of {L} layers x {S} tokens", flush=True)
+    print(f"cfg4 cache test fused={fused} offload={offload}: prefill of {L} layers x {S} tokens", flush=True)
     for layer in range(L):
         k = torch.randn(B, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16)
         v = torch.randn(B, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16)
@@ -75,7 +76,7 @@ def test_cfg4_decode_steps_match_simulation(fused, host_gather, monkeypatch):
     cache.prefill_all_layers_done()
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
-    assert cache._device_gather == (not host_gather)
+    assert cache._offload == offload
     assert cache.cpu_restore_k.shape[0] > 6 * L * (AUDIO - AUDIO // CHUNK * KEEP) // 2  # most class-B audio on host
     sim = DecodeSimulation(cache, [(TEXT, TEXT + AUDIO)])
     scale = D ** -0.5

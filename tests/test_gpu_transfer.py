@@ -1,0 +1,100 @@
+"""The host->device transfer engine (``wnw_h2d_*``): the planned host ranges
+land bit-exact in the device rows of their transfer order, group by group,
+over several consecutive starts (the two staging pairs in turn, the second
+reuse of a pair after its copies finish), with empty ranges and groups, and
+argument errors are refused without starting anything.  The reference's
+counterpart is the planner's gather into staging plus one side-stream copy
+(src/algorithms/wnw_cpp/code/planner.cpp:113-122,
+src/algorithms/wnw/code/cache.py:868-881); the expected rows here are the
+host rows themselves, indexed in numpy."""
+import numpy as np
+import pytest
+import torch
+
+from wnw_amd import _lib
+from wnw_amd.wnw.transfer import HostToDevice
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _host_rows(rng, n):
+    a = rng.integers(0, 1 << 16, (n, D), dtype=np.uint16)
+    t = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    return a, t.pin_memory()
+
+
+def _case(rng, host_rows, n_ranges, n_groups):
+    starts = rng.integers(0, host_rows - 300, n_ranges)
+    lens = rng.integers(0, 300, n_ranges)
+    lens[rng.random(n_ranges) < 0.1] = 0  # some empty ranges
+    ranges = np.stack([starts, starts + lens], 1).astype(np.int32)
+    cuts = np.sort(rng.integers(0, n_ranges + 1, n_groups - 1))
+    bounds = [0] + cuts.tolist() + [n_ranges]
+    return ranges, bounds
+
+
+def test_ranges_land_in_transfer_order_over_several_starts():
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(5)
+    hk_np, hk = _host_rows(rng, 20000)
+    hv_np, hv = _host_rows(rng, 20000)
+    eng = HostToDevice(workers=4)
+    stream = torch.cuda.Stream(device=dev)
+    stg = [(torch.empty(60000, D, dtype=torch.bfloat16, pin_memory=True),
+            torch.empty(60000, D, dtype=torch.bfloat16, pin_memory=True)) for _ in range(2)]
+    outs = []
+    for job in range(5):
+        ranges, bounds = _case(rng, 20000, int(rng.integers(1, 200)), int(rng.integers(1, 9)))
+        total = int((ranges[:, 1] - ranges[:, 0]).sum())
+        with torch.cuda.stream(stream):
+            dk = torch.empty(max(total, 1), D, dtype=torch.bfloat16, device=dev)
+            dv = torch.empty_like(dk)
+        sk, sv = stg[job % 2]
+        print(f"job {job}: {len(ranges)} ranges, {len(bounds) - 1} groups, {total} rows", flush=True)
+        eng.start(hk, hv, torch.from_numpy(ranges), bounds, sk, sv, dk, dv, stream)
+        compute = torch.cuda.current_stream(dev)
+        for g in range(len(bounds) - 1):
+            eng.wait(g, compute)
+        got_k = dk[:total].clone()  # on the compute stream, after every group's copy
+        got_v = dv[:total].clone()
+        outs.append((ranges, got_k, got_v))
+    eng.join()
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    for ranges, got_k, got_v in outs:
+        idx = np.concatenate([np.arange(s, e) for s, e in ranges]) if len(ranges) else np.zeros(0, np.int64)
+        np.testing.assert_array_equal(got_k.cpu().view(torch.int16).numpy().view(np.uint16), hk_np[idx])
+        np.testing.assert_array_equal(got_v.cpu().view(torch.int16).numpy().view(np.uint16), hv_np[idx])
+    eng.close()
+
+
+def test_arguments_are_checked():
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(6)
+    _, hk = _host_rows(rng, 1000)
+    _, hv = _host_rows(rng, 1000)
+    sk = torch.empty(100, D, dtype=torch.bfloat16, pin_memory=True)
+    sv = torch.empty(100, D, dtype=torch.bfloat16, pin_memory=True)
+    dk = torch.empty(100, D, dtype=torch.bfloat16, device=dev)
+    dv = torch.empty_like(dk)
+    s = torch.cuda.current_stream(dev)
+    eng = HostToDevice(workers=2)
+    ok = torch.tensor([[0, 10], [20, 30]], dtype=torch.int32)
+    with pytest.raises(_lib.WnwError):  # groups do not end at n_ranges
+        eng.start(hk, hv, ok, [0, 1], sk, sv, dk, dv, s)
+    with pytest.raises(_lib.WnwError):  # a range past the host rows
+        eng.start(hk, hv, torch.tensor([[990, 1010]], dtype=torch.int32), [0, 1], sk, sv, dk, dv, s)
+    with pytest.raises(_lib.WnwError):  # more rows than staging holds
+        eng.start(hk, hv, torch.tensor([[0, 200]], dtype=torch.int32), [0, 1], sk, sv, dk, dv, s)
+    with pytest.raises(_lib.WnwError):  # pageable staging
+        eng.start(hk, hv, ok, [0, 2], torch.empty(100, D, dtype=torch.bfloat16), sv, dk, dv, s)
+    eng.start(hk, hv, ok, [0, 1, 2], sk, sv, dk, dv, s)
+    with pytest.raises(_lib.WnwError):  # a group the job does not have
+        eng.wait(2, s)
+    eng.wait(0, s)
+    eng.wait(1, s)
+    eng.join()
+    torch.cuda.synchronize()
+    eng.close()

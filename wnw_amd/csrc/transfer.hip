@@ -1,0 +1,295 @@
+// Host->device transfer of a plan's offloaded rows through the copy engines
+// (host code only; no kernels).
+//
+// Reference: the offload channel of the WnW caches -- the planner gathers
+// the plan's host ranges into pinned staging (src/algorithms/wnw_cpp/code/
+// planner.cpp:113-122) and the cache copies the staging rows to the device
+// on a side stream and makes the rebuild wait for it
+// (src/algorithms/wnw/code/cache.py:716-721, :868-881).  There the gather
+// runs on one thread and one copy carries every layer's rows, so the first
+// layer's rebuild waits for the whole transfer.
+//
+// Here the ranges (in transfer order: layer, sample, head, segment) are
+// split into groups of consecutive layers.  A background thread per
+// engine walks the groups: a pool of worker threads memcpys the group's
+// ranges into the staging rows (ranges split evenly over the workers,
+// written with streaming stores: the staging is read by the DMA engines
+// only), then
+// the thread issues two hipMemcpyAsync (K and V) of the group's staging
+// rows into the same rows of the device buffers, and records an event.  A
+// layer's rebuild waits for its group's event only, so later groups' host
+// gathers and copies overlap earlier layers' compute, and the copies run on
+// the DMA engines: unlike a kernel reading pinned host memory, they leave
+// the compute kernels' memory traffic alone.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <condition_variable>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "hostcopy.h"
+#include "wnw_common.h"
+
+namespace {
+
+constexpr int kMaxGroups = 64;
+
+struct Job {
+  const char* host_k = nullptr;
+  const char* host_v = nullptr;
+  char* stg_k = nullptr;
+  char* stg_v = nullptr;
+  char* dev_k = nullptr;
+  char* dev_v = nullptr;
+  std::vector<int32_t> ranges;        // [n, 2] host rows, in staging order
+  std::vector<int64_t> dst;           // [n + 1] staging / device row of each range
+  std::vector<int64_t> group_ranges;  // [groups + 1] range index bounds
+  int64_t row_bytes = 0;
+  hipStream_t stream = nullptr;
+  int device = 0;
+  int parity = 0;
+};
+
+}  // namespace
+
+struct wnw_h2d {
+  std::vector<std::thread> workers;
+  std::thread lead;
+  std::mutex mu;
+  std::condition_variable cv_job, cv_task, cv_task_done, cv_issued;
+  bool stop = false;
+  // the current job: queued by start, walked by the lead thread
+  bool job_pending = false, job_running = false;
+  Job job;
+  int issued = -1;     // groups of the current job whose copies are issued
+  int groups = 0;
+  int error = WNW_OK;  // first HIP error of the current job
+  char error_msg[256] = "";  // its text (error strings are per thread: re-raised by wait / join)
+  // the worker task of the lead thread: one group's ranges
+  uint64_t task_seq = 0;
+  int task_group = -1;
+  int task_done = 0;
+  hipEvent_t events[2][kMaxGroups] = {};
+  int last_groups[2] = {0, 0};  // groups of the last job of each parity (0: none yet)
+  int parity = 0;
+  int n_workers = 0;
+};
+
+namespace {
+
+void copy_ranges(const Job& j, int64_t r0, int64_t r1) {
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t s = j.ranges[2 * r], n = (int64_t)j.ranges[2 * r + 1] - s;
+    const int64_t d = j.dst[r];
+    wnw::stream_copy(j.stg_k + d * j.row_bytes, j.host_k + s * j.row_bytes, n * j.row_bytes);
+    wnw::stream_copy(j.stg_v + d * j.row_bytes, j.host_v + s * j.row_bytes, n * j.row_bytes);
+  }
+  wnw::stream_fence();  // the streaming stores are visible before the copy engine reads the staging
+}
+
+// Worker w copies its share of the current task's group.
+void worker_loop(wnw_h2d* x, int w) {
+  uint64_t seen = 0;
+  for (;;) {
+    int g;
+    {
+      std::unique_lock<std::mutex> lk(x->mu);
+      x->cv_task.wait(lk, [&] { return x->stop || x->task_seq != seen; });
+      if (x->stop) return;
+      seen = x->task_seq;
+      g = x->task_group;
+    }
+    const Job& j = x->job;
+    const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
+    const int64_t n = b - a, W = x->n_workers;
+    copy_ranges(j, a + n * w / W, a + n * (w + 1) / W);
+    {
+      std::lock_guard<std::mutex> lk(x->mu);
+      if (++x->task_done == W) x->cv_task_done.notify_one();
+    }
+  }
+}
+
+void lead_loop(wnw_h2d* x) {
+  for (;;) {
+    {
+      std::unique_lock<std::mutex> lk(x->mu);
+      x->cv_job.wait(lk, [&] { return x->stop || x->job_pending; });
+      if (x->stop) return;
+      x->job_pending = false;
+      x->job_running = true;
+    }
+    const Job& j = x->job;
+    hipError_t e = hipSetDevice(j.device);
+    // the staging pair and events of this parity were last used two jobs
+    // ago: its copies must be done before the gather overwrites the staging
+    // (the events record in stream order, so the last one covers them all)
+    if (e == hipSuccess && x->last_groups[j.parity] > 0)
+      e = hipEventSynchronize(x->events[j.parity][x->last_groups[j.parity] - 1]);
+    for (int g = 0; g < x->groups; ++g) {
+      {
+        std::unique_lock<std::mutex> lk(x->mu);
+        x->task_group = g;
+        x->task_done = 0;
+        ++x->task_seq;
+        x->cv_task.notify_all();
+        x->cv_task_done.wait(lk, [&] { return x->task_done == x->n_workers; });
+      }
+      const int64_t d0 = j.dst[j.group_ranges[g]], d1 = j.dst[j.group_ranges[g + 1]];
+      const size_t bytes = (size_t)((d1 - d0) * j.row_bytes);
+      if (e == hipSuccess && bytes > 0)
+        e = hipMemcpyAsync(j.dev_k + d0 * j.row_bytes, j.stg_k + d0 * j.row_bytes, bytes, hipMemcpyHostToDevice,
+                           j.stream);
+      if (e == hipSuccess && bytes > 0)
+        e = hipMemcpyAsync(j.dev_v + d0 * j.row_bytes, j.stg_v + d0 * j.row_bytes, bytes, hipMemcpyHostToDevice,
+                           j.stream);
+      if (e == hipSuccess) e = hipEventRecord(x->events[j.parity][g], j.stream);
+      {
+        std::lock_guard<std::mutex> lk(x->mu);
+        if (e != hipSuccess && x->error == WNW_OK) {
+          snprintf(x->error_msg, sizeof(x->error_msg), "h2d: %s (%d)", hipGetErrorString(e), (int)e);
+          x->error = WNW_EHIP;
+        }
+        x->issued = g;
+        x->cv_issued.notify_all();
+      }
+    }
+    {
+      std::lock_guard<std::mutex> lk(x->mu);
+      x->last_groups[j.parity] = x->groups;
+      x->job_running = false;
+      x->cv_issued.notify_all();
+    }
+  }
+}
+
+// Blocks until the previous job is fully issued.
+void join_locked(wnw_h2d* x, std::unique_lock<std::mutex>& lk) {
+  x->cv_issued.wait(lk, [&] { return !x->job_pending && !x->job_running; });
+}
+
+}  // namespace
+
+extern "C" wnw_h2d* wnw_h2d_create(int n_workers) {
+  if (n_workers < 1 || n_workers > 64) {
+    wnw::set_error("h2d: n_workers must be in [1, 64], got %d", n_workers);
+    return nullptr;
+  }
+  wnw_h2d* x = new wnw_h2d();
+  for (int p = 0; p < 2; ++p)
+    for (int g = 0; g < kMaxGroups; ++g) {
+      if (hipEventCreateWithFlags(&x->events[p][g], hipEventDisableTiming) != hipSuccess) {
+        wnw::set_error("h2d: event creation failed");
+        for (int q = 0; q <= p; ++q)
+          for (int h = 0; h < kMaxGroups; ++h)
+            if (x->events[q][h]) (void)hipEventDestroy(x->events[q][h]);
+        delete x;
+        return nullptr;
+      }
+    }
+  x->n_workers = n_workers;
+  for (int w = 0; w < n_workers; ++w) x->workers.emplace_back(worker_loop, x, w);
+  x->lead = std::thread(lead_loop, x);
+  return x;
+}
+
+extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
+  if (!x) return;
+  {
+    std::unique_lock<std::mutex> lk(x->mu);
+    join_locked(x, lk);
+    x->stop = true;
+  }
+  x->cv_job.notify_all();
+  x->cv_task.notify_all();
+  x->lead.join();
+  for (auto& t : x->workers) t.join();
+  for (int p = 0; p < 2; ++p)
+    for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->events[p][g]);
+  delete x;
+}
+
+extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v, int64_t host_rows,
+                             const int32_t* ranges, int64_t n_ranges, const int64_t* group_ranges, int n_groups,
+                             void* stg_k, void* stg_v, int64_t stg_rows, void* dev_k, void* dev_v, int64_t dev_rows,
+                             int64_t row_bytes, void* stream) {
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  WNW_CHECK_ARG(n_groups >= 1 && n_groups <= kMaxGroups, "h2d: n_groups must be in [1, %d]", kMaxGroups);
+  WNW_CHECK_ARG(n_ranges >= 0 && row_bytes > 0, "h2d: bad sizes");
+  WNW_CHECK_ARG(group_ranges && group_ranges[0] == 0 && group_ranges[n_groups] == n_ranges,
+                "h2d: group bounds must run from 0 to n_ranges");
+  for (int g = 0; g < n_groups; ++g)
+    WNW_CHECK_ARG(group_ranges[g] <= group_ranges[g + 1], "h2d: group bounds decrease");
+  WNW_CHECK_ARG(n_ranges == 0 || (ranges && host_k && host_v && stg_k && stg_v && dev_k && dev_v),
+                "h2d: null pointer argument");
+  Job j;
+  j.ranges.assign(ranges, ranges + 2 * n_ranges);
+  j.dst.resize(n_ranges + 1);
+  j.dst[0] = 0;
+  for (int64_t r = 0; r < n_ranges; ++r) {
+    const int64_t s = j.ranges[2 * r], e = j.ranges[2 * r + 1];
+    WNW_CHECK_ARG(s >= 0 && e >= s && e <= host_rows, "h2d: range %lld = [%lld, %lld) outside %lld host rows",
+                  (long long)r, (long long)s, (long long)e, (long long)host_rows);
+    j.dst[r + 1] = j.dst[r] + (e - s);
+  }
+  WNW_CHECK_ARG(j.dst[n_ranges] <= stg_rows && j.dst[n_ranges] <= dev_rows,
+                "h2d: %lld rows do not fit staging (%lld) and device (%lld) buffers", (long long)j.dst[n_ranges],
+                (long long)stg_rows, (long long)dev_rows);
+  j.group_ranges.assign(group_ranges, group_ranges + n_groups + 1);
+  j.host_k = (const char*)host_k;
+  j.host_v = (const char*)host_v;
+  j.stg_k = (char*)stg_k;
+  j.stg_v = (char*)stg_v;
+  j.dev_k = (char*)dev_k;
+  j.dev_v = (char*)dev_v;
+  j.row_bytes = row_bytes;
+  j.stream = (hipStream_t)stream;
+  WNW_CHECK_HIP(hipGetDevice(&j.device), "h2d: hipGetDevice");
+  {
+    std::unique_lock<std::mutex> lk(x->mu);
+    join_locked(x, lk);  // the previous job's groups are issued; its events stay valid (other parity)
+    x->parity ^= 1;
+    j.parity = x->parity;
+    x->job = std::move(j);
+    x->groups = n_groups;
+    x->issued = -1;
+    x->error = WNW_OK;
+    x->error_msg[0] = 0;
+    x->job_pending = true;
+  }
+  x->cv_job.notify_all();
+  return WNW_OK;
+}
+
+extern "C" int wnw_h2d_wait(wnw_h2d* x, int group, void* stream) {
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  hipEvent_t ev;
+  {
+    std::unique_lock<std::mutex> lk(x->mu);
+    WNW_CHECK_ARG(group >= 0 && group < x->groups, "h2d: group %d outside [0, %d)", group, x->groups);
+    x->cv_issued.wait(lk, [&] { return x->issued >= group || (!x->job_pending && !x->job_running); });
+    if (x->error != WNW_OK) {
+      wnw::set_error("%s", x->error_msg);
+      return x->error;
+    }
+    if (x->issued < group) {
+      wnw::set_error("h2d: group %d was never issued", group);
+      return WNW_EINVAL;
+    }
+    ev = x->events[x->job.parity][group];
+  }
+  WNW_CHECK_HIP(hipStreamWaitEvent((hipStream_t)stream, ev, 0), "h2d: hipStreamWaitEvent");
+  return WNW_OK;
+}
+
+extern "C" int wnw_h2d_join(wnw_h2d* x) {
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  std::unique_lock<std::mutex> lk(x->mu);
+  join_locked(x, lk);
+  if (x->error != WNW_OK) wnw::set_error("%s", x->error_msg);
+  return x->error;
+}

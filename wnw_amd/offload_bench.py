@@ -6,8 +6,11 @@ layer are class A (full KV, scored); the other six are class B: they keep
 5 rows of each 256-token segment plus the text, and the rest of the audio
 lives in pinned host memory as 256-token chunks.  After every decode step
 the planner picks the top-8 chunks from the class-A scores of that step and
-the cache fetches the newly chosen ones with an asynchronous host->device
-copy on a side stream, overlapped with the next step's compute.  As in the
+the cache fetches the newly chosen ones on a side stream in groups of
+layers, overlapped with the next step's compute: through the path
+``WNW_OFFLOAD`` names ("device", the default: a gather kernel reading pinned
+host memory; "copy": host gather threads and DMA copies); the other path is
+timed too.  As in the
 reference (src/algorithms/wnw/code/cache.py:609-630) the choice is per
 sample, shared by every class-B head and layer.
 
@@ -18,11 +21,13 @@ prefill scores U(0, 1), seed 0; the step inputs (q and the new K/V row of
 every layer) are made before the timed region.
 
 Reported: wall time per decode step (the host is part of the step: the
-cache runs its Python and planner logic per layer), host->device bytes
-per step (the cache's own transfer events), the time a plain pinned copy of
-those bytes takes, the step time of the same run without offload (top-k 0:
-nothing is ever fetched) and the difference of the two step times (what
-offload adds per step: planning, fetch and rebuilds, net of overlap).
+cache runs its Python and planner logic per layer) through the default path
+and through the other one, host->device bytes per step (the cache's own
+transfer events), the time a plain pinned copy of those bytes takes on the
+copy engine, the step time of the same run without offload (top-k 0:
+nothing is ever fetched) and the difference of the default and no-offload
+step times (what offload adds per step: planning, fetch and rebuilds, net of
+overlap).
 """
 from __future__ import annotations
 
@@ -147,16 +152,40 @@ def _copy_time(nbytes: int, dev) -> float:
     return e0.elapsed_time(e1) * 1e-3 / 5
 
 
-def run(steps: int, warmup: int) -> dict:
+def _offload_step(mode: str, steps: int, warmup: int, dev):
+    """Step time with the host rows loaded through ``mode`` (WNW_OFFLOAD)."""
+    import os
+
     import torch
 
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    cache = _prefilled_cache(TOP_K, dev)
+    old = os.environ.get("WNW_OFFLOAD")
+    os.environ["WNW_OFFLOAD"] = mode
+    try:
+        cache = _prefilled_cache(TOP_K, dev)
+    finally:
+        if old is None:
+            del os.environ["WNW_OFFLOAD"]
+        else:
+            os.environ["WNW_OFFLOAD"] = old
+    assert cache._offload == mode
     host_rows = int(cache.cpu_restore_k.shape[0])
     t_step, c2g_per_step, n_load_steps = _timed(cache, steps, warmup, dev)
     del cache
     torch.cuda.empty_cache()
+    return t_step, c2g_per_step, n_load_steps, host_rows
+
+
+def run(steps: int, warmup: int) -> dict:
+    import os
+
+    import torch
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    default = os.environ.get("WNW_OFFLOAD", "device")
+    other = "copy" if default == "device" else "device"
+    t_step, c2g_per_step, n_load_steps, host_rows = _offload_step(default, steps, warmup, dev)
+    t_other, _, _, _ = _offload_step(other, steps, warmup, dev)
     base = _prefilled_cache(0, dev)
     t_base, _, _ = _timed(base, steps, warmup, dev)
     del base
@@ -169,6 +198,8 @@ def run(steps: int, warmup: int) -> dict:
         "config": {"workload": "cfg4-offload-22500tok-b1", "layers": L, "batch": B, "hq": HQ, "hkv": HKV,
                    "head_dim": D, "audio": AUDIO, "chunk": CHUNK, "top_k_chunks": TOP_K,
                    "class_b_keep_per_chunk": KEEP_PER_SEG, "host_rows": host_rows},
+        "offload_path": default,
+        f"ms_per_step_{other}_path": round(t_other * 1e3, 3),
         "ms_per_step_no_offload": round(t_base * 1e3, 3),
         "h2d_MB_per_step": round(c2g_per_step / 1e6, 2),
         "steps_with_loads": n_load_steps,

@@ -20,11 +20,14 @@ decode step, per layer (cache.py:487-566)
     ``decode_after_attn``       class-A scores per KV group
                                 (``fused_score_accumulate``);
 after the last layer (cache.py:568-607)
-    ``decode_all_layers_done``  chunk means of the score accumulator ->
-                                top-k per sample -> native plan -> gather of
-                                the host rows into pinned staging -> H2D copy
-                                on a side stream with an event the next
-                                step's first rebuild waits for.
+    ``decode_all_layers_done``  chunk means and top-k per sample (one
+                                launch, read back through pinned memory) ->
+                                native plan -> the host rows to the device
+                                in groups of layers (``WNW_OFFLOAD``:
+                                "device", a gather kernel reading pinned
+                                memory; "copy", the transfer engine's gather
+                                threads and DMA copies), each group with an
+                                event its layers' rebuilds wait for.
 
 Prefill (cache.py:236-390) builds the flat layout: class-A KV heads keep
 every token, other heads keep their per-segment top-k audio tokens plus all
@@ -39,16 +42,18 @@ logical view is the reference's (``cu_seqlens_k``, ``seq_lens``, row order
 within a segment); only the physical placement differs, so every attention
 launch takes ``seg_base``, and ``dense_kv(layer)`` gathers the reference's
 dense rows for a caller that needs them.  Appends are in place (one row per
-segment, no copy of the layer).  A plan's changed segments are compacted
-into the pool's free tail (relocated; the old rows are left behind), and
-only when the tail is used up is the layer copied into a fresh pool.
+segment, no copy of the layer).  A pool with host rows ends in a flip region
+of two halves; a plan compacts the layer's class-B segments with their loads
+into the half they do not occupy (every class-B segment, so the other half
+is wholly free again), and only a plan that does not fit a half, or an
+append beyond a segment's room, copies the layer into a fresh pool.
 ``slack_rows=0`` keeps the reference's dense layout, where every append
 copies the layer out of place (``interleave_append``) and every plan
 rebuilds it (``rebuild_append_kv``).
 
-One deliberate difference: before the host refills the pinned staging
-buffer for a new plan it waits for the previous plan's H2D copy (the
-reference overwrites staging that an in-flight copy may still read).
+One deliberate difference: before the host refills a pinned staging buffer
+it waits for the copies that last read it (the reference overwrites staging
+that an in-flight copy may still read).
 """
 from __future__ import annotations
 
@@ -66,6 +71,7 @@ from ..kv.fused_attn import decode_attn, q1_decode_attn, q1_decode_attn_score
 from ..kv.kernels import append_inplace, interleave_append
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
+from .transfer import HostToDevice
 from .kernels import (chunk_topk, compact_segments, fused_score_accumulate, gather_host_rows, host_rows_readable,
                       rebuild_append_kv)
 
@@ -272,6 +278,7 @@ class WnWCache(FlatVarlenCache):
     def _clear_pending_rebuild_state(self) -> None:
         L = self.num_layers
         self._pending_layer_events: list = [None] * L  # per layer: the copy of its loaded rows
+        self._waited_groups: set = set()  # transfer-engine groups the compute stream already waits for
         self._pending_gpu_k: Tensor | None = None
         self._pending_gpu_v: Tensor | None = None
         self._pending_load_starts: list = [None] * L
@@ -472,16 +479,32 @@ class WnWCache(FlatVarlenCache):
 
     def _half_rows(self, layer_idx: int, lens: list[int]) -> int:
         """Rows of each half of the flip region after the segments, where
-        plans put the class-B segments (with their slack): ``tail_factor``
-        times the room those segments take, at least ``tail_rows_min``, when
-        there are host rows to load, else none (no plan changes a layout
-        without them)."""
+        plans put the class-B segments (with their slack): room for every
+        class-B segment at its length plus the most host rows it can have
+        loaded at once (``top_k_chunks`` x (1 + ``eviction_lag``) of its
+        sample's widest chunks of its largest offloaded segment, capped by
+        its offloaded rows), and at least ``tail_factor`` times their present
+        room and ``tail_rows_min``; none without host rows (no plan changes a
+        layout then) or with ``tail_factor`` and ``tail_rows_min`` both 0 (a
+        pool without a flip region: every plan rebuilds the layer)."""
         if self.cpu_restore_k is None or self.cpu_restore_k.shape[0] == 0:
+            return 0
+        if self.tail_factor == 0 and self.tail_rows_min == 0:
             return 0
         H = self.num_kv_heads
         heads = set(self._class_b_heads_by_layer[layer_idx])
-        room = sum(_round8(n + self.slack_rows) for f, n in enumerate(lens) if f % H in heads)
-        return _round8(max(self.tail_rows_min, self.tail_factor * room))
+        k, lag = self.config.top_k_chunks, self.config.eviction_lag
+        room = grown = 0
+        for f, n in enumerate(lens):
+            if f % H not in heads:
+                continue
+            b, h = divmod(f, H)
+            rows = [m.cpu_end - m.cpu_start for m in self.restore_meta[layer_idx][b][h] if m is not None]
+            width = max((len(c) for c in self.chunk_to_segs[b]), default=0)
+            extra = min(sum(rows), k * (1 + lag) * width * max(rows)) if rows else 0
+            room += _round8(n + self.slack_rows)
+            grown += _round8(n + extra + self.slack_rows)
+        return _round8(max(self.tail_rows_min, self.tail_factor * room, grown))
 
     def _relayout(self, layer_idx: int, plan: dict | None = None) -> None:
         """Copy layer ``layer_idx`` into a fresh pool: every segment's rows in
@@ -582,13 +605,29 @@ class WnWCache(FlatVarlenCache):
         # two pinned staging pairs, used in turn and grown on demand: a plan's
         # gather waits only for the copy that used its pair two plans ago
         self._staging = [None, None]
-        self._staging_events: list = [None, None]
         self._staging_turn = 0
-        # the device reads the pinned restore rows itself unless they are not
-        # readable or WNW_HOST_GATHER=1 asks for the host gather + staging copy
-        self._gather_launches = 6  # launches (events) per plan: copy/compute overlap vs launch cost
-        self._device_gather = os.environ.get("WNW_HOST_GATHER", "0") != "1" and \
-            self.cpu_restore_k.shape[0] > 0 and host_rows_readable(self.cpu_restore_k, self.cpu_restore_v)
+        # the offload channel (WNW_OFFLOAD): "device" (default), a gather
+        # kernel reading the pinned restore rows itself (the faster transfer:
+        # the CUs' reads of host memory outrun the copy engine, but they slow
+        # the compute kernels that run meanwhile); "copy", the transfer
+        # engine -- host gather threads and DMA copies per group of layers,
+        # which leave the compute kernels' memory traffic alone
+        self._load_groups = 8  # groups (copies + events) per plan: copy/compute overlap vs per-copy cost
+        mode = os.environ.get("WNW_OFFLOAD", "device")
+        if mode not in ("copy", "device"):
+            raise ValueError(f"WNW_OFFLOAD must be 'copy' or 'device', got {mode!r}")
+        if mode == "device" and self.cpu_restore_k.shape[0] > 0 and \
+                not host_rows_readable(self.cpu_restore_k, self.cpu_restore_v):
+            mode = "copy"  # the device cannot read these host rows: through the copy engines
+        self._offload = mode
+        self._h2d = None
+        self._staging_rows_hint = self._plan_rows_bound()
+        if mode == "copy" and self._staging_rows_hint > 0:
+            # both pairs now, touched once: a first write into fresh pinned
+            # pages is several times slower than the gathers that follow
+            dt = self.cpu_restore_k.dtype
+            self._staging = [tuple(torch.zeros(self._staging_rows_hint, self.head_dim, dtype=dt, pin_memory=True)
+                                   for _ in range(2)) for _ in range(2)]
         N = B * H
         self._plan_out = dict(
             load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
@@ -816,13 +855,14 @@ class WnWCache(FlatVarlenCache):
         and no search for room is needed.  A layer whose block does not fit
         a half gets a fresh pool instead (``_relayout`` with the plan)."""
         o = self._plan_out
+        eo = o["evict_offsets_2d"]
+        changed = ((o["load_lens_2d"] > 0) | (eo[:, 1:] > eo[:, :-1])).any(dim=1).tolist()
         bases_all, caps_all, lens_all, src_all, cu_all = [], [], [], [], []
         for l in range(self.num_layers):
-            ll, eo = o["load_lens_2d"][l], o["evict_offsets_2d"][l]
             lens = [x - 1 for x in new_lens_all[l]]  # the step's append comes after the move
             bases, caps = list(self._base_list[l]), list(self._cap_list[l])
             kind = "none"
-            if bool(((ll > 0) | (eo[1:] > eo[:-1])).any()):
+            if changed[l]:
                 t0 = t = self._half_start[l] + self._flip[l] * self._half_size[l]
                 for f in self._classb_segs[l]:
                     bases[f], caps[f] = t, _round8(lens[f] + self.slack_rows)
@@ -849,7 +889,7 @@ class WnWCache(FlatVarlenCache):
         compact_segments(k, v, k, v, self._classb_segs_dev[l], self.seg_base[l], sdev[l], bdev[l], ldev[l],
                          self._pending_gpu_k, self._pending_gpu_v, self._pending_load_starts[l],
                          self._pending_load_lens[l], self._pending_evict_offsets[l], self._pending_evict_starts[l],
-                         self._pending_evict_ends[l], max(lens[f] for f in segs))
+                         self._pending_evict_ends[l], max(lens[f] for f in segs), check=False)
         self.seg_base[l], self.seg_cap[l] = bdev[l], cdev[l]
         self._base_list[l], self._cap_list[l] = bases, caps
         self._flip[l] ^= 1
@@ -947,13 +987,21 @@ class WnWCache(FlatVarlenCache):
             self._prepare_pending_rebuild()
 
     def _prepare_pending_rebuild(self) -> None:
-        """cache.py:756-889 with the native plan: per-layer descriptors on the
-        device, host rows gathered into pinned staging and copied on the
-        transfer stream."""
+        """cache.py:756-889 with the native plan: the host rows' transfer
+        started first (its gather threads run while the rest is prepared),
+        then the per-layer descriptors on the device."""
         total, ev_s, ev_e, ranges = self._plan_result
         self._clear_pending_rebuild_state()
         o = self._plan_out
         dev = self.device
+        dt = self.layer_k[0].dtype
+        if total > 0 and self._offload == "device":
+            self._gather_loads_on_device(total, ranges, o["load_lens_2d"])
+        elif total > 0:
+            self._copy_loads(total, ranges, o["load_lens_2d"])
+        else:
+            self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
+            self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
         i32 = torch.int32
         ls, ll, cun = (_to_device(o["load_starts_2d"], i32, dev), _to_device(o["load_lens_2d"], i32, dev),
                        _to_device(o["cu_new_2d"], i32, dev))
@@ -972,7 +1020,6 @@ class WnWCache(FlatVarlenCache):
         self._segments_changed_ranges = ranges
         if self.slack_layout:
             self._plan_slack_moves(new_lens)
-        dt = self.layer_k[0].dtype
         if total > 0 and self._record_plan_transfers and self.stats.enabled:
             # cache.py:816-820: host rows loaded per sample (K and V)
             per_row = self.head_dim * 2 * self.cpu_restore_k.element_size()
@@ -980,25 +1027,6 @@ class WnWCache(FlatVarlenCache):
             for b, n in enumerate(lens.tolist()):
                 if n > 0:
                     self.stats.record_cpu_gpu_transfer(b, c2g_tokens=int(n), c2g_bytes=int(n) * per_row)
-        if total > 0 and self._device_gather:
-            self._gather_loads_on_device(total, ranges, o["load_lens_2d"])
-        elif total > 0:
-            stg_k, stg_v = self._staging_pair(total)
-            self._planner.gather_restore()
-            stream = self._get_transfer_stream()
-            ev = torch.cuda.Event()
-            with torch.cuda.stream(stream):
-                self._pending_gpu_k = stg_k[:total].to(dev, non_blocking=True)
-                self._pending_gpu_v = stg_v[:total].to(dev, non_blocking=True)
-                ev.record(stream)
-            compute = torch.cuda.current_stream(dev)
-            self._pending_gpu_k.record_stream(compute)
-            self._pending_gpu_v.record_stream(compute)
-            self._pending_layer_events = [ev] * self.num_layers
-            self._staging_events[self._staging_turn ^ 1] = ev
-        else:
-            self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
-            self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
 
     def _gather_loads_on_device(self, total: int, ranges: Tensor, load_lens_2d: Tensor) -> None:
         """The plan's host ranges read by the device straight from the pinned
@@ -1016,15 +1044,13 @@ class WnWCache(FlatVarlenCache):
         compute = torch.cuda.current_stream(dev)
         stream = self._get_transfer_stream()
         events = [None] * self.num_layers
-        per_launch = max(1, -(-self.num_layers // self._gather_launches))
         with torch.cuda.stream(stream):
             rg = _to_device(ranges, ranges.dtype, dev)
             do = _to_device(dst, dst.dtype, dev)
             pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
             pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
             r0 = 0
-            for l0 in range(0, self.num_layers, per_launch):
-                l1 = min(l0 + per_launch, self.num_layers)
+            for l0, l1 in self._group_layers():
                 r1 = bounds[l1 - 1]
                 if r1 > r0:
                     gather_host_rows(self.cpu_restore_k, self.cpu_restore_v, rg, do, r0, r1, pk, pv)
@@ -1037,24 +1063,90 @@ class WnWCache(FlatVarlenCache):
         self._pending_gpu_k, self._pending_gpu_v = pk, pv
         self._pending_layer_events = events
 
-    def _staging_pair(self, rows: int) -> tuple[Tensor, Tensor]:
-        """The next staging pair, holding at least `rows` rows, handed to the
-        planner.  Its previous copy (two plans ago) must have left it; the
-        pair grows to the next power of two (cache.py:128-134 grows its one
-        staging buffer the same way)."""
+    def _layer_groups(self, ranges: Tensor, load_lens_2d: Tensor) -> tuple[list[int], list[int]]:
+        """Groups of consecutive layers for a plan's loads: the range index
+        bounds of each group and each layer's group.  Ranges are in transfer
+        order (layer, sample, head, segment), so each layer's ranges are
+        contiguous."""
+        lens = (ranges[:, 1] - ranges[:, 0]).to(torch.int64)
+        dst = torch.zeros(ranges.shape[0] + 1, dtype=torch.int64)
+        torch.cumsum(lens, 0, out=dst[1:])
+        ends = torch.searchsorted(dst, torch.cumsum(load_lens_2d.to(torch.int64).sum(dim=1), 0)).tolist()
+        bounds, group_of = [0], []
+        for l0, l1 in self._group_layers():
+            bounds.append(ends[l1 - 1])
+            group_of += [len(bounds) - 2] * (l1 - l0)
+        return bounds, group_of
+
+    def _group_layers(self) -> list[tuple[int, int]]:
+        """Layer spans of the load groups: a short first group (the first
+        layer's rows arrive after a small gather and copy), the other layers
+        split evenly over the remaining groups."""
+        L, n = self.num_layers, max(1, min(self._load_groups, self.num_layers))
+        if n == 1:
+            return [(0, L)]
+        first = max(1, L // (2 * n))
+        cuts = [0, first] + [first + (L - first) * g // (n - 1) for g in range(1, n)]
+        return [(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
+
+    def _copy_loads(self, total: int, ranges: Tensor, load_lens_2d: Tensor) -> None:
+        """The plan's host ranges to the device through the transfer engine:
+        gathered into a pinned staging pair and copied by the DMA engines on
+        the transfer stream, group of layers by group, a layer's rebuild
+        waiting for its own group only.  Returns without waiting."""
+        dev = self.device
+        bounds, group_of = self._layer_groups(ranges, load_lens_2d)
+        stg_k, stg_v = self._engine_staging(total)
+        stream = self._get_transfer_stream()
+        with torch.cuda.stream(stream):  # the copies into them follow on this stream
+            pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
+            pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
+        compute = torch.cuda.current_stream(dev)
+        pk.record_stream(compute)
+        pv.record_stream(compute)
+        if self._h2d is None:
+            self._h2d = HostToDevice()
+        self._h2d.start(self.cpu_restore_k, self.cpu_restore_v, ranges.to(torch.int32), bounds, stg_k, stg_v, pk, pv,
+                        stream)
+        self._pending_gpu_k, self._pending_gpu_v = pk, pv
+        self._pending_layer_events = [("h2d", g) for g in group_of]
+
+    def _plan_rows_bound(self) -> int:
+        """An upper bound on the host rows one plan loads: per (layer, sample,
+        class-B head), at most ``top_k_chunks`` chunks of the sample's widest
+        chunk, each segment with that head's most offloaded rows (capped by
+        the head's offloaded rows).  Sizes the staging pairs once."""
+        k = self.config.top_k_chunks
+        total = 0
+        for l in range(self.num_layers):
+            for b in range(self.batch_size):
+                width = max((len(c) for c in self.chunk_to_segs[b]), default=0)
+                for h in range(self.num_kv_heads):
+                    rows = [m.cpu_end - m.cpu_start for m in self.restore_meta[l][b][h] if m is not None]
+                    if rows:
+                        total += min(sum(rows), k * width * max(rows))
+        return total
+
+    def _engine_staging(self, rows: int) -> tuple[Tensor, Tensor]:
+        """The next of two pinned staging pairs (used in turn, one per plan,
+        as the engine alternates: a plan's gather waits inside the engine for
+        the copies that used its pair two plans ago), holding at least
+        ``rows`` rows: first sized by the bound on a plan's rows, grown to the
+        next power of two past it (cache.py:128-134 grows its one staging
+        buffer the same way)."""
         i = self._staging_turn
         self._staging_turn ^= 1
-        if self._staging_events[i] is not None:
-            self._staging_events[i].synchronize()
-            self._staging_events[i] = None
         pair = self._staging[i]
         if pair is None or pair[0].shape[0] < rows:
-            cap = min(1 << max(0, rows - 1).bit_length(), max(rows, self.cpu_restore_k.shape[0]))
+            if pair is not None:  # the engine's copies may still read the old pair: drain them before it goes
+                self._h2d.join()
+                self._get_transfer_stream().synchronize()
+            cap = max(rows, self._staging_rows_hint) if pair is None else \
+                min(1 << max(0, rows - 1).bit_length(), max(rows, self.cpu_restore_k.shape[0]))
             dt = self.cpu_restore_k.dtype
             pair = (torch.empty(cap, self.head_dim, dtype=dt, pin_memory=True),
                     torch.empty(cap, self.head_dim, dtype=dt, pin_memory=True))
             self._staging[i] = pair
-        self._planner.set_restore_buffers(self.cpu_restore_k, self.cpu_restore_v, pair[0], pair[1])
         return pair
 
     def _rebuild_append_layer(self, layer_idx: int, new_k: Tensor, new_v: Tensor):
@@ -1086,9 +1178,15 @@ class WnWCache(FlatVarlenCache):
         """The compute stream waits for the copy of this layer's loaded rows
         (cache.py:719-721 waits once for the whole transfer)."""
         ev = self._pending_layer_events[layer_idx]
-        if ev is not None:
+        if ev is None:
+            return
+        if isinstance(ev, tuple):  # a group of the transfer engine: one wait per group
+            if ev[1] not in self._waited_groups:
+                self._h2d.wait(ev[1], torch.cuda.current_stream(self.device))
+                self._waited_groups.add(ev[1])
+        else:
             torch.cuda.current_stream(self.device).wait_event(ev)
-            self._pending_layer_events[layer_idx] = None
+        self._pending_layer_events[layer_idx] = None
 
     def _finish_layer(self, layer_idx, k, v, cu_new, new_lens) -> None:
         self.layer_k[layer_idx], self.layer_v[layer_idx] = k, v

@@ -159,37 +159,45 @@ def compact_segments(
     *,
     new_k: torch.Tensor | None = None,
     new_v: torch.Tensor | None = None,
+    check: bool = True,
 ) -> None:
     """Compaction + load (+ optional append) of the listed segments between
     physically addressed layouts (``wnw_compact_segments``).  With
     ``new_k=None`` no row is appended: the compaction step of the reference's
-    out-of-place fallback (src/algorithms/wnw/code/cache.py:891-1010)."""
-    _lib.require_gpu(src_k, src_v, dst_k, dst_v, seg_list, src_base, src_len, dst_base, new_len, load_starts,
-                     load_lens, evict_offsets)
+    out-of-place fallback (src/algorithms/wnw/code/cache.py:891-1010).
+    ``check=False`` skips the Python-side dtype / device / shape checks (the
+    library still checks every bound): for callers whose arguments are
+    contiguous tensors of the right dtypes by construction, per layer and
+    step."""
     n = src_base.numel()
-    d = src_k.shape[1]
-    for name, t, dt in (("seg_list", seg_list, torch.int32), ("src_base", src_base, torch.int64),
-                        ("src_len", src_len, torch.int32), ("dst_base", dst_base, torch.int64),
-                        ("new_len", new_len, torch.int32), ("load_starts", load_starts, torch.int32),
-                        ("load_lens", load_lens, torch.int32), ("evict_offsets", evict_offsets, torch.int32)):
-        if t.dtype != dt:
-            raise _lib.WnwError(f"{name} must be {dt}")
-    if evict_offsets.numel() != n + 1:
-        raise _lib.WnwError("evict_offsets must be int32 [N+1]")
+    if check:
+        _lib.require_gpu(src_k, src_v, dst_k, dst_v, seg_list, src_base, src_len, dst_base, new_len, load_starts,
+                         load_lens, evict_offsets)
+        for name, t, dt in (("seg_list", seg_list, torch.int32), ("src_base", src_base, torch.int64),
+                            ("src_len", src_len, torch.int32), ("dst_base", dst_base, torch.int64),
+                            ("new_len", new_len, torch.int32), ("load_starts", load_starts, torch.int32),
+                            ("load_lens", load_lens, torch.int32), ("evict_offsets", evict_offsets, torch.int32)):
+            if t.dtype != dt:
+                raise _lib.WnwError(f"{name} must be {dt}")
+        if evict_offsets.numel() != n + 1:
+            raise _lib.WnwError("evict_offsets must be int32 [N+1]")
+        keep = [t.contiguous() if t is not None and t.numel() else None for t in
+                (new_k, new_v, load_k, load_v, seg_list, src_base, src_len, dst_base, new_len, load_starts,
+                 load_lens, evict_offsets, evict_starts, evict_ends)]
+        _lib.ensure_init(src_k.device)
+    else:
+        keep = [t if t is not None and t.numel() else None for t in
+                (new_k, new_v, load_k, load_v, seg_list, src_base, src_len, dst_base, new_len, load_starts,
+                 load_lens, evict_offsets, evict_starts, evict_ends)]
     with_new = new_k is not None
-    keep = [t.contiguous() if t is not None and t.numel() else None for t in
-            (new_k, new_v, load_k, load_v, seg_list, src_base, src_len, dst_base, new_len, load_starts, load_lens,
-             evict_offsets, evict_starts, evict_ends)]
     nk, nv, lk, lv, sl, sb, sn, db, nl, ls, ll, eo, es, ee = keep
     n_ev = 0 if es is None else es.numel()
-    _lib.ensure_init(src_k.device)
+    P = _lib.ptr
     _lib.check(_lib.lib().wnw_compact_segments(
-        _lib.ptr(src_k), _lib.ptr(src_v), _lib.ptr(dst_k), _lib.ptr(dst_v), _lib.ptr(nk), _lib.ptr(nv),
-        _lib.ptr(lk), _lib.ptr(lv), _lib.ptr(sl), seg_list.numel(), n, int(max_new_len), _lib.ptr(sb),
-        _lib.ptr(sn), _lib.ptr(db), _lib.ptr(nl), _lib.ptr(ls), _lib.ptr(ll), _lib.ptr(eo), _lib.ptr(es),
-        _lib.ptr(ee), n_ev, 1 if with_new else 0, src_k.shape[0], dst_k.shape[0],
-        0 if lk is None else lk.shape[0], d, _lib.dtype_code(src_k.dtype), _lib.stream_of(src_k.device)),
-        "compact_segments")
+        P(src_k), P(src_v), P(dst_k), P(dst_v), P(nk), P(nv), P(lk), P(lv), P(sl), seg_list.numel(), n,
+        int(max_new_len), P(sb), P(sn), P(db), P(nl), P(ls), P(ll), P(eo), P(es), P(ee), n_ev, 1 if with_new else 0,
+        src_k.shape[0], dst_k.shape[0], 0 if lk is None else lk.shape[0], src_k.shape[1],
+        _lib.dtype_code(src_k.dtype), _lib.stream_of(src_k.device)), "compact_segments")
 
 
 def chunk_topk(score_acc: torch.Tensor, score_offsets: torch.Tensor, chunk_offsets: torch.Tensor,

@@ -1,0 +1,79 @@
+"""Binding of the host->device transfer engine (``wnw_h2d_*``, csrc/transfer.hip).
+
+The offload channel of the reference (src/algorithms/wnw_cpp/code/
+planner.cpp:113-122 gathers a plan's host ranges into pinned staging;
+src/algorithms/wnw/code/cache.py:716-721, :868-881 copies the staging rows to
+the device on a side stream and waits for them before the rebuild), done by
+a background engine: worker threads gather the ranges group by group (groups
+of consecutive layers), each group is copied by the DMA engines as soon as it
+is gathered, and a layer waits only for its own group's copy.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from .. import _lib
+
+
+class HostToDevice:
+    """One engine (a lead thread and ``workers`` gather threads) per cache."""
+
+    def __init__(self, workers: int | None = None):
+        if workers is None:
+            # the host's cores less a few for the caller's thread, the engine's
+            # lead thread and the runtime
+            workers = int(os.environ.get("WNW_H2D_WORKERS", "0")) or max(1, min(12, (os.cpu_count() or 2) - 4))
+        self._h = _lib.lib().wnw_h2d_create(int(workers))
+        if not self._h:
+            raise _lib.WnwError("wnw_h2d_create: " + _lib.lib().wnw_last_error().decode(errors="replace"))
+        self.workers = int(workers)
+        self._keep = ()
+
+    def start(self, host_k: torch.Tensor, host_v: torch.Tensor, ranges: torch.Tensor, group_ranges: list[int],
+              stg_k: torch.Tensor, stg_v: torch.Tensor, dev_k: torch.Tensor, dev_v: torch.Tensor,
+              stream: torch.cuda.Stream) -> None:
+        """Gathers rows ``ranges[r, 0] .. ranges[r, 1]`` of the pinned host
+        arrays into consecutive staging rows and copies them to the same rows
+        of ``dev_k`` / ``dev_v`` on ``stream``, group ``g`` being ranges
+        ``group_ranges[g] .. group_ranges[g + 1]``.  Returns at once; the
+        previous start must be issued (it waits for that)."""
+        for t in (host_k, host_v, stg_k, stg_v):
+            if t.device.type != "cpu" or not t.is_pinned() or not t.is_contiguous():
+                raise _lib.WnwError("host and staging rows must be contiguous pinned tensors")
+        if ranges.dtype != torch.int32 or ranges.device.type != "cpu" or ranges.dim() != 2 or ranges.shape[1] != 2:
+            raise _lib.WnwError("ranges must be a CPU int32 [n, 2] tensor")
+        row_bytes = host_k.shape[1] * host_k.element_size()
+        if host_k.shape != host_v.shape or stg_k.shape[1:] != host_k.shape[1:] or dev_k.shape[1:] != host_k.shape[1:] \
+                or dev_k.shape != dev_v.shape or stg_k.shape != stg_v.shape or dev_k.dtype != host_k.dtype:
+            raise _lib.WnwError("host, staging and device rows must have one row shape and dtype")
+        rg = ranges.contiguous()
+        gr = (ctypes.c_int64 * len(group_ranges))(*group_ranges)
+        self._keep = (rg, gr)  # the engine copies both at start; kept for symmetry with the pointers' lifetime
+        _lib.check(_lib.lib().wnw_h2d_start(
+            self._h, _lib.ptr(host_k), _lib.ptr(host_v), host_k.shape[0], _lib.ptr(rg), rg.shape[0], gr,
+            len(group_ranges) - 1, _lib.ptr(stg_k), _lib.ptr(stg_v), stg_k.shape[0], _lib.ptr(dev_k), _lib.ptr(dev_v),
+            dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream)), "h2d start")
+
+    def wait(self, group: int, stream: torch.cuda.Stream | None = None) -> None:
+        """``stream`` (default: the current one) waits for group ``group``'s
+        copy; the host blocks only until that copy is issued."""
+        s = stream if stream is not None else torch.cuda.current_stream()
+        _lib.check(_lib.lib().wnw_h2d_wait(self._h, int(group), ctypes.c_void_p(s.cuda_stream)), "h2d wait")
+
+    def join(self) -> None:
+        """Blocks until every group of the last start is issued."""
+        _lib.check(_lib.lib().wnw_h2d_join(self._h), "h2d join")
+
+    def close(self) -> None:
+        if self._h:
+            _lib.lib().wnw_h2d_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
