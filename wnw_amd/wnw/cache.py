@@ -167,9 +167,10 @@ class WnWCache(FlatVarlenCache):
         if slack_rows < 0:
             raise ValueError("slack_rows must be >= 0")
         self.slack_rows = int(slack_rows)
-        # flip region of a pool with host rows: two halves of max(tail_rows_min,
-        # tail_factor x the class-B rows) each; a plan moves the layer's
-        # class-B segments into the half they do not occupy
+        # flip region of a pool with host rows: two halves (sized by _half_rows:
+        # the plan's bound on the class-B rows, at least tail_rows_min and
+        # tail_factor x their present room); a plan moves the layer's class-B
+        # segments into the half they do not occupy
         self.tail_rows_min = 1024
         self.tail_factor = 2
         # layout changes so far: (fresh pools, fresh pools applying a plan,
