@@ -451,6 +451,24 @@ def test_fused_append_table_pass(gpu, n_seg):
     _check_append(_append_case(gpu, lens, 4, 128, "bfloat16", seed=n_seg), "bfloat16")
 
 
+@pytest.mark.parametrize("case", ["direct", "table_pass"])
+def test_fused_append_pieces_of_whole_steps(gpu, case):
+    """Pieces that end their segment with a multiple of 16 old rows (the
+    kernel then cuts their first step to 15 rows, so the step that ends the
+    segment has room for the new row).  direct: 64 segments of 256 rows,
+    R = 16384 = 1024 * 16, so with the usual grid of 256 workgroups (4 waves
+    each) every wave's range is 16 rows and every segment ends a full 16-row
+    piece.  table_pass: 2000 segments of 16, 32 or 48 rows, most of them
+    whole inside a wave's range."""
+    if case == "direct":
+        lens = [256] * 64
+    else:
+        lens = [int(x) for x in np.random.default_rng(5).choice([16, 32, 48], 2000)]
+    for dtype in ("bfloat16", "float16"):
+        print(f"pieces of whole steps: {case} {dtype}", flush=True)
+        _check_append(_append_case(gpu, lens, 4, 128, dtype, seed=len(lens)), dtype)
+
+
 @pytest.mark.parametrize("dtype,G,D", [("float32", 4, 128), ("bfloat16", 16, 128), ("bfloat16", 4, 256)])
 def test_fused_append_other_kernels(gpu, dtype, G, D):
     """Where the streaming kernel does not apply (fp32, group > 8, head_dim

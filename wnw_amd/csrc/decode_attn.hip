@@ -24,9 +24,10 @@
 // new row, new_k/new_v[s], at physical row base[s] + len_old[s] (len_old from
 // cu).  The split and the stream cover the old rows only, exactly as without
 // the append; the first step of every piece also copies its segment's new
-// row into LDS beside q, and the wave that finishes a segment folds that row
-// into its softmax state (one more logit and one more V row) before the
-// state is written or merged.  The new rows are stored into the pools, and
+// row into LDS beside q, and the step that ends a segment takes that row as
+// one of its own rows.  Such a step always has room for it: a piece that
+// ends its segment and holds a multiple of 16 rows starts with a 15-row
+// step.  The new rows are stored into the pools, and
 // cu_out = cu + arange(n_seg + 1) written, at the end of the kernel, where
 // no wait of the stream waits for their acknowledgement.
 //
@@ -132,9 +133,14 @@ static constexpr int kSplitWaves = 4;
 __device__ __forceinline__ int64_t unit_start(int64_t u, int64_t R, uint64_t inv) {
   return (int64_t)__umul64hi((uint64_t)(u * R), inv);
 }
-// The workgroup whose row range holds logical row j (P <= R).
+// The workgroup whose row range holds logical row j (P <= R):
+// floor(x / R) for x = (j + 1) P - 1, by a correctly rounded double division
+// instead of a 64-bit integer one (~170 instructions).  Exact for
+// 0 <= x < 2^52: when x / R = n - d is not an integer, d >= 1 / R, while
+// the rounding error is at most n 2^-53 < 1 / R (n R <= x + R < 2^53), so the
+// quotient never rounds up to n.  Here x < 2^31 * 2^14.
 __device__ __forceinline__ int64_t owner_of(int64_t j, int64_t R, int64_t P) {
-  return ((j + 1) * P - 1) / R;
+  return (int64_t)floor((double)((j + 1) * P - 1) / (double)R);
 }
 __device__ __forceinline__ int64_t effective_wgs(int64_t R) {
   return R > 0 ? min((int64_t)gridDim.x, R) : 0;
@@ -426,9 +432,13 @@ __device__ __forceinline__ void combine_pieces(const AttnParams& p, int D, int64
       u32x2 ml[QC];
 #pragma unroll
       for (int k = 0; k < QC; ++k) {
-        const int kk = min(q0 + k, np - 1);  // past np: a repeat, masked below
-        a[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, i4 * 16, kk * GD * 4, kSc1));
-        ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rm, g * 8, kk * G * 8, kSc1);
+        a[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ml[k] = u32x2{0u, 0u};
+        if (q0 + k < np) {  // wave-uniform: no wait between the loads
+          a[k] = __builtin_bit_cast(f32x4,
+                                    __builtin_amdgcn_raw_buffer_load_b128(ra, i4 * 16, (q0 + k) * GD * 4, kSc1));
+          ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rm, g * 8, (q0 + k) * G * 8, kSc1);
+        }
       }
       float Mc = M;
 #pragma unroll
@@ -989,7 +999,7 @@ struct SStep {
   int32_t s, nrows, seg_len, qslot;
   int32_t first, last, whole;
   int32_t t0, alen;  // audio index of the first row; audio rows whose logits are kept (0: none)
-  int32_t ends_seg;  // APPEND: the step ends its segment (its new row is folded in after it)
+  int32_t ends_seg;  // APPEND: the step ends its segment (fewer than 16 old rows; the new row is added)
   int32_t wr;        // APPEND: the segment's lane in the walk's window (its capacity)
 };
 
@@ -1158,6 +1168,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   int cur_s = 0, cur_len = 0, piece_no = 0, cur_a0 = 0, cur_al = 0, cur_k = 0;
   int64_t cur_b = 0, cur_lo = 0, pb = 0, pe = 0, irow = 0;
   bool cur_whole = false, have = false;
+  // APPEND: the piece ends its segment with a multiple of 16 rows, so its
+  // first step takes 15: the step that ends the segment then always has room
+  // for the new row
+  bool short_first = false;
   auto next_piece = [&]() {
     while (mask == 0) {
       wb += 64;
@@ -1175,7 +1189,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
     cur_lo = __builtin_amdgcn_readlane(llo, k);
     cur_len = __builtin_amdgcn_readlane(llen, k);
-    cur_k = k;  // the segment's lane in the window (its capacity is read when its new row is folded)
+    cur_k = k;  // the segment's lane in the window (its capacity is read when its new row is kept)
     if (XL) {
       cur_a0 = __builtin_amdgcn_readlane(la0, k);
       cur_al = __builtin_amdgcn_readlane(lal, k);
@@ -1183,6 +1197,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     pb = max(cur_lo, W0);
     pe = min(cur_lo + cur_len, W1);
     cur_whole = cur_lo >= W0 && cur_lo + cur_len <= W1;
+    short_first = APPEND && pe == cur_lo + cur_len && ((pe - pb) & (kSRows - 1)) == 0;
     irow = pb;
     have = true;
   };
@@ -1193,8 +1208,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     st.seg_lo = cur_lo;
     st.seg_len = cur_len;
     st.row0 = cur_b + (irow - cur_lo);
-    st.nrows = (int32_t)min((int64_t)kSRows, pe - irow);
     st.first = irow == pb;
+    st.nrows = APPEND && st.first && short_first ? kSRows - 1 : (int32_t)min((int64_t)kSRows, pe - irow);
     st.whole = cur_whole;
     st.qslot = piece_no & 1;
     if (XL) {
@@ -1203,7 +1218,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     }
     st.ends_seg = APPEND && irow + st.nrows == cur_lo + cur_len;
     st.wr = cur_k;
-    irow += kSRows;
+    irow += st.nrows;
     st.last = irow >= pe;
     if (st.last) {
       ++piece_no;
@@ -1253,44 +1268,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   int64_t c_b = 0;
   u32x4 qb[NC];
 
-  // APPEND, a segment whose last step is full (16 old rows): its new row
-  // (behind q in the piece's slot) folded into the softmax state once the
-  // step is done -- one more logit per head (the dot product of q's chunks in
-  // this lane with the row's, summed over the head's four lanes) and one more
-  // V row (this lane's accumulator elements 16 t + 4 lq + i).  Every LDS read
-  // is issued before the math.  (A last step with room takes the row as one
-  // of its own rows instead; see process.)
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  auto fold_new_row = [&](const SStep& st) {
-    const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;  // K row, then V row
-    u32x4 kk[NC];
-    u32x2 vv[NTD];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) kk[c] = *(const u32x4*)(nrow + (4 * c + lq) * 16);
-#pragma unroll
-    for (int t = 0; t < NTD; ++t) vv[t] = *(const u32x2*)(nrow + RB + (16 * t + 4 * lq) * 2);
-    float dot = 0.f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        dot += Ops::to_f32(qb[c][j] & 0xffffu) * Ops::to_f32(kk[c][j] & 0xffffu) +
-               Ops::to_f32(qb[c][j] >> 16) * Ops::to_f32(kk[c][j] >> 16);
-    dot = sum_x32(sum_x16(dot));
-    const float xn = lc < G ? dot * p.scale_log2 : -INFINITY;
-    const float m_new = fmaxf(m_run, xn);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    const float pw = __builtin_amdgcn_exp2f(xn - m_new);
-    m_run = m_new;
-    l_run = l_run * alpha + (lq == 0 ? pw : 0.f);
-#pragma unroll
-    for (int t = 0; t < NTD; ++t) {
-      acc[t][0] = acc[t][0] * alpha + pw * Ops::to_f32(vv[t].x & 0xffffu);
-      acc[t][1] = acc[t][1] * alpha + pw * Ops::to_f32(vv[t].x >> 16);
-      acc[t][2] = acc[t][2] * alpha + pw * Ops::to_f32(vv[t].y & 0xffffu);
-      acc[t][3] = acc[t][3] * alpha + pw * Ops::to_f32(vv[t].y >> 16);
-    }
-  };
   // APPEND: a segment's new row kept for the pools (stored after the hand-off)
   // when the segment has room for it; the capacity, loaded with the table,
   // is read only now.  The row goes after the segment's old rows.
@@ -1326,8 +1303,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
       for (int c = 0; c < NC; ++c)
         qb[c] = lc < G ? *(const u32x4*)(qsl + lc * RB + (4 * c + lq) * 16) : u32x4{0, 0, 0, 0};
     }
-    // APPEND: a step that ends its segment with fewer than 16 old rows takes
-    // the segment's new row (behind q in the piece's slot) as row nrows:
+    // APPEND: the step that ends its segment (fewer than 16 old rows, by the
+    // cut of the piece's steps) takes the segment's new row (behind q in the
+    // piece's slot) as row nrows:
     // its K chunks now, swizzled like the loaded rows, its V chunks after
     // V's wait.  The step's DMA has landed, and the buffer is this wave's
     // until the step after next is issued.
@@ -1413,7 +1391,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     __builtin_amdgcn_sched_barrier(0);
     if (st.last) {
       if (APPEND && st.ends_seg) {
-        if (!add_row) fold_new_row(st);
         keep_new_row(st);
       }
       const float l_tot = sum_x32(sum_x16(l_run));
