@@ -142,25 +142,27 @@ __device__ __forceinline__ int64_t unit_start(int64_t u, int64_t R, uint64_t inv
 __device__ __forceinline__ int64_t owner_of(int64_t j, int64_t R, int64_t P) {
   return (int64_t)floor((double)((j + 1) * P - 1) / (double)R);
 }
-__device__ __forceinline__ int64_t effective_wgs(int64_t R) {
-  return R > 0 ? min((int64_t)gridDim.x, R) : 0;
+__device__ __forceinline__ int64_t effective_wgs(int64_t R, int64_t grid = gridDim.x) {
+  return R > 0 ? min(grid, R) : 0;
 }
 // Start of split unit u (of P * kSplitWaves) for R rows: the reciprocal
 // when every workgroup of the grid takes part (R >= gridDim.x), else a
 // division (tiny launches).
-__device__ __forceinline__ int64_t split_start(int64_t u, int64_t R, int64_t P, uint64_t inv) {
-  if (P == (int64_t)gridDim.x && inv != 0) return unit_start(u, R, inv);
+__device__ __forceinline__ int64_t split_start(int64_t u, int64_t R, int64_t P, uint64_t inv,
+                                              int64_t grid = gridDim.x) {
+  if (P == grid && inv != 0) return unit_start(u, R, inv);
   return (u * R) / (P * kSplitWaves);
 }
 // This workgroup's logical row range [B0, B1) for R rows over P workgroups.
-__device__ __forceinline__ void wg_range(int64_t R, int64_t P, uint64_t inv, int64_t& B0, int64_t& B1) {
+__device__ __forceinline__ void wg_range(int64_t R, int64_t P, uint64_t inv, int64_t& B0, int64_t& B1,
+                                         int64_t grid = gridDim.x) {
   const int64_t pid = blockIdx.x;
   if (pid >= P) {
     B0 = B1 = 0;
     return;
   }
-  B0 = split_start(pid * kSplitWaves, R, P, inv);
-  B1 = split_start((pid + 1) * kSplitWaves, R, P, inv);
+  B0 = split_start(pid * kSplitWaves, R, P, inv, grid);
+  B1 = split_start((pid + 1) * kSplitWaves, R, P, inv, grid);
 }
 
 // APPEND, a segment with no old rows: its only row is the new one, so every
@@ -1005,16 +1007,36 @@ struct SStep {
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
 // APPEND: append new_k / new_v[s] to every segment first (fused append).
-template <typename T, int D, int NW, int QD, bool XL, bool APPEND>
-// The fields read first lead the argument list as scalars: the build
-// preloads the first 16 argument dwords into SGPRs at dispatch
-// (-amdgpu-kernarg-preload-count), so the segment table and the first steps
-// are addressed without a kernel-argument load; aggregates are not preloaded.
-__global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_arg, const void* k_arg, const void* v_arg,
-                                                               const int32_t* cu_arg, const int64_t* base_arg,
-                                                               const int32_t* cap_arg, uint64_t inv_arg,
-                                                               int32_t nseg_arg, int32_t g_arg,
+template <typename T, int D, int NW, int QD, bool XL, bool APPEND, bool DIRECT>
+// The fields read first lead the argument list as scalars: the build asks
+// for 16 preloaded argument dwords (-amdgpu-kernarg-preload-count), of which
+// the hardware delivers 14 in SGPRs at dispatch (the other two user SGPRs
+// hold the argument pointer).  Those 14 are exactly the table, the tensors,
+// the segment count and the group size packed with the grid size
+// (gpack = G | grid << 8), so the table load is the kernel's first
+// instruction of note and no argument or implicit-argument load (gridDim)
+// precedes it; the split reciprocal and the aggregate are loaded and arrive
+// while the table load is in flight.
+__global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* cu_arg, const int64_t* base_arg,
+                                                               const int32_t* cap_arg, const void* q_arg,
+                                                               const void* k_arg, const void* v_arg,
+                                                               int32_t nseg_arg, int32_t gpack_arg, uint64_t inv_arg,
                                                                AttnParams p) {
+  // DIRECT (n_seg <= 64, n_seg >= 1): lane s's segment bounds, loaded before
+  // anything else (clamped lanes load segment n_seg - 1 and are masked by
+  // the walk)
+  int32_t t_lo = 0, t_hi = 0, t_cap = 0;
+  int64_t t_base = 0;
+  if constexpr (DIRECT) {
+    const int si = min((int)(threadIdx.x & 63), nseg_arg - 1);
+    t_lo = cu_arg[si];
+    t_hi = cu_arg[si + 1];
+    if (base_arg) t_base = base_arg[si];
+    if (APPEND) t_cap = cap_arg[si];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t grid = (int64_t)((uint32_t)gpack_arg >> 8);
+  const int32_t g_arg = gpack_arg & 0xff;
   p.q = q_arg;
   p.k = k_arg;
   p.v = v_arg;
@@ -1078,7 +1100,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   // the workgroup's checks of the table (and the outputs of empty or
   // invalid segments) follow once those loads are out.  More segments: the
   // workgroup pass of schedule() first, with its LDS cache of the bounds.
-  const bool direct = p.n_seg <= 64;
+  // DIRECT is chosen by the host (n_seg <= 64); the two prologues are
+  // separate instances, so neither carries the other's code and registers.
+  constexpr bool direct = DIRECT;
+  if (DIRECT && p.n_seg > 64) {
+    if (tid == 0 && blockIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    return;
+  }
   const int64_t KV = p.phys_rows;
   int64_t R = 0, B0 = 0, B1 = 0;
   int s_first, s_last;
@@ -1135,12 +1163,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
           lal = sl.ring_alen[s % kRing];
         }
       } else {
-        const int32_t lo = p.cu[s], hi = p.cu[s + 1];
-        lb = p.base ? p.base[s] : (int64_t)lo;
+        // DIRECT: the one window, s = lane, loaded at entry
+        const int32_t lo = DIRECT ? t_lo : p.cu[s], hi = DIRECT ? t_hi : p.cu[s + 1];
+        lb = p.base ? (DIRECT ? t_base : p.base[s]) : (int64_t)lo;
         llo = lo;
         llen = hi - lo;
         lneg = llen < 0;
-        if (APPEND) lcap = p.cap[s];
+        if (APPEND) lcap = DIRECT ? t_cap : p.cap[s];
         if (XL && p.xmask[s % p.Hkv]) {
           la0 = p.audio_s[s / p.Hkv];
           lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
@@ -1157,10 +1186,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     // sit on the start-up path; the workgroup's follow once the first steps
     // are issued.
     R = max((int64_t)0, (int64_t)__builtin_amdgcn_readlane(llo + llen, p.n_seg - 1));
-    P_ = effective_wgs(R);
+    P_ = effective_wgs(R, grid);
     if ((int64_t)blockIdx.x < P_) {
-      W0 = split_start((int64_t)blockIdx.x * NW + w, R, P_, p.split_inv);
-      W1 = split_start((int64_t)blockIdx.x * NW + w + 1, R, P_, p.split_inv);
+      W0 = split_start((int64_t)blockIdx.x * NW + w, R, P_, p.split_inv, grid);
+      W1 = split_start((int64_t)blockIdx.x * NW + w + 1, R, P_, p.split_inv, grid);
     }
     window_mask();
   }
@@ -1440,7 +1469,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
   bool hB = hA && gen(sB);
   if (hB) issue(sB, 1);
   if (direct) {
-    wg_range(R, P_, p.split_inv, B0, B1);
+    wg_range(R, P_, p.split_inv, B0, B1, grid);
     if (tid == 0) {  // read by the merge and the hand-off, after barriers
       sl.R = R;
       sl.KV = KV;
@@ -1464,7 +1493,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const void* q_a
     const bool any_bad = __ballot(bad) != 0;
     if (lane == 0) sl.order_bad = any_bad;
     if (in && !seg_valid(llo, len, lb, R, KV)) {
-      const bool owner = (si % (int)gridDim.x) == (int)blockIdx.x;
+      const bool owner = (si % (int)grid) == (int)blockIdx.x;
       if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
       if (APPEND && len == 0 && !lneg) {  // only the new row: it is the output
         if (owner) append_only_segment<T>(p, D, si, lb, 1 <= lcap && lb >= 0 && lb < KV);
@@ -1909,18 +1938,27 @@ static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex&
 // Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
 // stream_lds_bytes (above 64 KB, so the limit is raised once per instance
 // and device).
-template <typename T, int D, int QD, bool XL, bool APPEND>
-static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+template <typename T, int D, int QD, bool XL, bool APPEND, bool DIRECT>
+static hipError_t launch_stream_k(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
   const int lds = stream_lds_bytes(D, kNW, stream_qslot(ap.G, D, APPEND), APPEND);
   static std::mutex mu;
   static std::vector<signed char> done;
   const hipError_t attr_err =
-      set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND>,
+      set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT>,
                          stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND));
   if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
-                     st, ap.q, ap.k, ap.v, ap.cu, ap.base, ap.cap, ap.split_inv, ap.n_seg, ap.G, ap);
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
+                     st, ap.cu, ap.base, ap.cap, ap.q, ap.k, ap.v, ap.n_seg,
+                     (int32_t)((uint32_t)ap.G | ((uint32_t)n_wg << 8)), ap.split_inv, ap);
   return hipGetLastError();
+}
+
+// Up to 64 segments the table is read by every wave directly (one lane per
+// segment); more take the workgroup scheduling pass.
+template <typename T, int D, int QD, bool XL, bool APPEND>
+static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+  return ap.n_seg <= 64 ? launch_stream_k<T, D, QD, XL, APPEND, true>(ap, n_wg, st)
+                        : launch_stream_k<T, D, QD, XL, APPEND, false>(ap, n_wg, st);
 }
 
 template <typename T, int D, int QD>
