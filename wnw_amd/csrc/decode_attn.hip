@@ -1037,6 +1037,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   __builtin_amdgcn_sched_barrier(0);
   const int64_t grid = (int64_t)((uint32_t)gpack_arg >> 8);
   const int32_t g_arg = gpack_arg & 0xff;
+  // The argument fields the range computation and the first steps use,
+  // loaded here while the table load is in flight: left to the compiler,
+  // their loads sit behind the table's wait, one more round trip each.
+  if constexpr (DIRECT)
+    asm volatile("" ::"s"(inv_arg), "s"(p.phys_rows), "s"(p.scale_log2), "s"(p.new_k), "s"(p.new_v));
   p.q = q_arg;
   p.k = k_arg;
   p.v = v_arg;
