@@ -27,18 +27,23 @@ class AttnWorkspace:
         self.device = device
         self.buf: torch.Tensor | None = None
         self.cleared_for = -1  # n_seg of the layout whose counters are known to be zero
+        self._need: dict[tuple, int] = {}  # bytes the library asks for, per layout
 
     def get(self, n_seg: int, group: int, head_dim: int, score: bool = False,
             max_audio: int = 0) -> tuple[torch.Tensor, int]:
         """Buffer and its size; ``score`` adds room for the softmax
         normalisers of ``wnw_decode_attn_score`` and, with ``max_audio`` > 0,
         for the logits of the scored audio rows."""
-        if score:
-            need = int(_lib.lib().wnw_decode_attn_score_workspace_bytes(n_seg, group, head_dim, max_audio))
-        else:
-            need = int(_lib.lib().wnw_decode_attn_workspace_bytes(n_seg, group, head_dim))
-        if need < 0:
-            raise _lib.WnwError("bad workspace query")
+        key = (n_seg, group, head_dim, score, max_audio)
+        need = self._need.get(key)
+        if need is None:
+            if score:
+                need = int(_lib.lib().wnw_decode_attn_score_workspace_bytes(n_seg, group, head_dim, max_audio))
+            else:
+                need = int(_lib.lib().wnw_decode_attn_workspace_bytes(n_seg, group, head_dim))
+            if need < 0:
+                raise _lib.WnwError("bad workspace query")
+            self._need[key] = need
         if self.buf is None or self.buf.numel() < need:
             size = max(need, 1 << 20)
             self.buf = torch.empty(size, dtype=torch.uint8, device=self.device)
@@ -84,6 +89,7 @@ def decode_attn(
     kernel: str = "auto",
     n_wg: int = 0,
     append: tuple | None = None,
+    validate: bool = True,
 ) -> torch.Tensor:
     """Decode attention with the layout extensions of this package.
 
@@ -101,6 +107,35 @@ def decode_attn(
     streaming kernel does both in one launch.  ``cu_new`` receives
     ``cu_k + arange(N + 1)``.
     """
+    if validate:
+        q_flat, cu_k = _check_attn(q_flat, k_flat, v_flat, cu_k, seg_base, total_rows)
+    nseg, g, d = q_flat.shape
+    if out is None:
+        out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
+    rows = k_flat.shape[0] if total_rows is None else int(total_rows)
+    _lib.ensure_init(q_flat.device)
+    ws = workspace if workspace is not None else workspace_for(q_flat.device)
+    buf, nbytes = ws.get(nseg, g, d)
+    if append is not None:
+        if kernel != "auto" or n_wg:
+            raise _lib.WnwError("the fused append runs the AUTO kernel choice and grid")
+        new_k, new_v, cu_new, seg_cap = (_check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base) if validate
+                                         else append)
+        _lib.check(_lib.lib().wnw_decode_attn_append(
+            _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
+            _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, rows, k_flat.shape[0], float(scale),
+            _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(buf), nbytes, _lib.stream_of(q_flat.device)),
+            "decode_attn_append")
+        return out
+    _lib.check(_lib.lib().wnw_decode_attn_ex(
+        _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base),
+        nseg, g, d, rows, k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out),
+        _lib.ptr(buf), nbytes, _KERNELS[kernel], int(n_wg), _lib.stream_of(q_flat.device)), "decode_attn")
+    return out
+
+
+def _check_attn(q_flat, k_flat, v_flat, cu_k, seg_base, total_rows):
+    """Validate decode_attn's tensors; returns q_flat and cu_k contiguous."""
     _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, seg_base)
     if q_flat.dim() != 3:
         raise _lib.WnwError(f"q_flat must be [N, G, D], got {tuple(q_flat.shape)}")
@@ -118,29 +153,7 @@ def decode_attn(
     if k_flat.shape[0] > 0 and (k_flat.stride(1) != 1 or k_flat.stride(0) != d or v_flat.stride(1) != 1
                                 or v_flat.stride(0) != d):
         raise _lib.WnwError("k_flat / v_flat rows must be contiguous [rows, D]")
-    q_flat = q_flat.contiguous()
-    cu_k = cu_k.contiguous()
-    if out is None:
-        out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
-    rows = k_flat.shape[0] if total_rows is None else int(total_rows)
-    _lib.ensure_init(q_flat.device)
-    ws = workspace if workspace is not None else workspace_for(q_flat.device)
-    buf, nbytes = ws.get(nseg, g, d)
-    if append is not None:
-        if kernel != "auto" or n_wg:
-            raise _lib.WnwError("the fused append runs the AUTO kernel choice and grid")
-        new_k, new_v, cu_new, seg_cap = _check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base)
-        _lib.check(_lib.lib().wnw_decode_attn_append(
-            _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
-            _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, rows, k_flat.shape[0], float(scale),
-            _lib.dtype_code(q_flat.dtype), _lib.ptr(out), _lib.ptr(buf), nbytes, _lib.stream_of(q_flat.device)),
-            "decode_attn_append")
-        return out
-    _lib.check(_lib.lib().wnw_decode_attn_ex(
-        _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(cu_k), _lib.ptr(seg_base),
-        nseg, g, d, rows, k_flat.shape[0], float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out),
-        _lib.ptr(buf), nbytes, _KERNELS[kernel], int(n_wg), _lib.stream_of(q_flat.device)), "decode_attn")
-    return out
+    return q_flat.contiguous(), cu_k.contiguous()
 
 
 def _check_append(append, nseg: int, d: int, dtype, cu_k, seg_base):
@@ -199,6 +212,7 @@ def q1_decode_attn_score(
     workspace: AttnWorkspace | None = None,
     keep_logits: bool = True,
     append: tuple | None = None,
+    validate: bool = True,
 ) -> torch.Tensor:
     """Attention output [nseg, G, D] plus class-A score accumulation.
 
@@ -213,32 +227,18 @@ def q1_decode_attn_score(
     rows for the scoring pass (workspace of n_seg * G * max_audio floats);
     without it the scoring pass reads the K rows again.  ``append`` as for
     ``decode_attn``: the step's rows are appended in place first (scores
-    then cover the appended segments).
+    then cover the appended segments).  ``validate=False`` skips the argument
+    checks for a caller whose tensors are known to satisfy them (the cache's
+    own, per layer and step).
     """
     del block_n
-    _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_accumulator,
-                     score_offsets, seg_base)
+    if validate:
+        q_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_offsets = _check_score(
+            q_flat, k_flat, v_flat, cu_k, ca_kv_mask, num_kv_heads, audio_starts, audio_ends, score_accumulator,
+            score_offsets, seg_base, total_rows)
     nseg, g, d = q_flat.shape
-    for name, t, n in (("ca_kv_mask", ca_kv_mask, num_kv_heads), ("audio_starts", audio_starts, nseg // num_kv_heads),
-                       ("audio_ends", audio_ends, nseg // num_kv_heads),
-                       ("score_offsets", score_offsets, nseg // num_kv_heads + 1)):
-        if t.dtype != torch.int32 or t.numel() != n:
-            raise _lib.WnwError(f"{name} must be int32 [{n}]")
-    if score_accumulator.dtype != torch.float32 or not score_accumulator.is_contiguous():
-        raise _lib.WnwError("score_accumulator must be a contiguous float32 tensor")
-    if k_flat.dim() != 2 or k_flat.shape[1] != d or v_flat.shape != k_flat.shape:
-        raise _lib.WnwError("k/v must be [rows, D] and equal")
-    if q_flat.dtype != k_flat.dtype or v_flat.dtype != k_flat.dtype:
-        raise _lib.WnwError("q, k and v must share a dtype")
-    if cu_k.dtype != torch.int32 or cu_k.numel() != nseg + 1:
-        raise _lib.WnwError("cu_k must be int32 [N+1]")
     if max_audio is None:
         max_audio = int((audio_ends - audio_starts).max().item()) if audio_ends.numel() else 0
-    if seg_base is not None and total_rows is None:
-        raise _lib.WnwError("total_rows (cu_k[-1]) is required with seg_base")
-    q_flat, cu_k = q_flat.contiguous(), cu_k.contiguous()
-    ca_kv_mask, audio_starts, audio_ends, score_offsets = (
-        t.contiguous() for t in (ca_kv_mask, audio_starts, audio_ends, score_offsets))
     if out is None:
         out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
     rows = k_flat.shape[0] if total_rows is None else int(total_rows)
@@ -246,7 +246,8 @@ def q1_decode_attn_score(
     ws = workspace if workspace is not None else workspace_for(q_flat.device)
     buf, nbytes = ws.get(nseg, g, d, score=True, max_audio=int(max_audio) if keep_logits else 0)
     if append is not None:
-        new_k, new_v, cu_new, seg_cap = _check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base)
+        new_k, new_v, cu_new, seg_cap = (_check_append(append, nseg, d, k_flat.dtype, cu_k, seg_base) if validate
+                                         else append)
         _lib.check(_lib.lib().wnw_decode_attn_score_append(
             _lib.ptr(q_flat), _lib.ptr(k_flat), _lib.ptr(v_flat), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
             _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, rows, k_flat.shape[0], float(scale),
@@ -262,3 +263,31 @@ def q1_decode_attn_score(
         _lib.ptr(score_offsets), score_accumulator.numel(), int(max_audio), _lib.ptr(buf), nbytes,
         _lib.stream_of(q_flat.device)), "q1_decode_attn_score")
     return out
+
+
+def _check_score(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, num_kv_heads, audio_starts, audio_ends,
+                 score_accumulator, score_offsets, seg_base, total_rows):
+    """Validate q1_decode_attn_score's tensors; returns the ones the launch
+    needs contiguous."""
+    _lib.require_gpu(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, audio_starts, audio_ends, score_accumulator,
+                     score_offsets, seg_base)
+    if q_flat.dim() != 3:
+        raise _lib.WnwError(f"q_flat must be [N, G, D], got {tuple(q_flat.shape)}")
+    nseg, g, d = q_flat.shape
+    for name, t, n in (("ca_kv_mask", ca_kv_mask, num_kv_heads), ("audio_starts", audio_starts, nseg // num_kv_heads),
+                       ("audio_ends", audio_ends, nseg // num_kv_heads),
+                       ("score_offsets", score_offsets, nseg // num_kv_heads + 1)):
+        if t.dtype != torch.int32 or t.numel() != n:
+            raise _lib.WnwError(f"{name} must be int32 [{n}]")
+    if score_accumulator.dtype != torch.float32 or not score_accumulator.is_contiguous():
+        raise _lib.WnwError("score_accumulator must be a contiguous float32 tensor")
+    if k_flat.dim() != 2 or k_flat.shape[1] != d or v_flat.shape != k_flat.shape:
+        raise _lib.WnwError("k/v must be [rows, D] and equal")
+    if q_flat.dtype != k_flat.dtype or v_flat.dtype != k_flat.dtype:
+        raise _lib.WnwError("q, k and v must share a dtype")
+    if cu_k.dtype != torch.int32 or cu_k.numel() != nseg + 1:
+        raise _lib.WnwError("cu_k must be int32 [N+1]")
+    if seg_base is not None and total_rows is None:
+        raise _lib.WnwError("total_rows (cu_k[-1]) is required with seg_base")
+    return (q_flat.contiguous(), cu_k.contiguous(), ca_kv_mask.contiguous(), audio_starts.contiguous(),
+            audio_ends.contiguous(), score_offsets.contiguous())

@@ -8,9 +8,9 @@ lives in pinned host memory as 256-token chunks.  After every decode step
 the planner picks the top-8 chunks from the class-A scores of that step and
 the cache fetches the newly chosen ones on a side stream in groups of
 layers, overlapped with the next step's compute: through the path
-``WNW_OFFLOAD`` names ("device", the default: a gather kernel reading pinned
-host memory; "copy": host gather threads and DMA copies); the other path is
-timed too.  As in the
+``WNW_OFFLOAD`` names ("copy", the default: host gather threads and DMA
+copies; "device": a gather kernel reading pinned host memory); the other path
+is timed too.  As in the
 reference (src/algorithms/wnw/code/cache.py:609-630) the choice is per
 sample, shared by every class-B head and layer.
 
@@ -182,7 +182,7 @@ def run(steps: int, warmup: int) -> dict:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    default = os.environ.get("WNW_OFFLOAD", "device")
+    default = os.environ.get("WNW_OFFLOAD", "copy")
     other = "copy" if default == "device" else "device"
     t_step, c2g_per_step, n_load_steps, host_rows = _offload_step(default, steps, warmup, dev)
     t_other, _, _, _ = _offload_step(other, steps, warmup, dev)

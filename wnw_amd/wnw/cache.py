@@ -24,10 +24,11 @@ after the last layer (cache.py:568-607)
                                 launch, read back through pinned memory) ->
                                 native plan -> the host rows to the device
                                 in groups of layers (``WNW_OFFLOAD``:
-                                "device", a gather kernel reading pinned
-                                memory; "copy", the transfer engine's gather
-                                threads and DMA copies), each group with an
-                                event its layers' rebuilds wait for.
+                                "copy", the default, the transfer engine's
+                                gather threads and DMA copies; "device", a
+                                gather kernel reading pinned memory), each
+                                group with an event its layers' rebuilds
+                                wait for.
 
 Prefill (cache.py:236-390) builds the flat layout: class-A KV heads keep
 every token, other heads keep their per-segment top-k audio tokens plus all
@@ -111,6 +112,26 @@ def _to_device(data, dtype: torch.dtype, device: torch.device) -> Tensor:
     staged = torch.empty(t.shape, dtype=dtype, pin_memory=True)
     staged.copy_(t)
     return staged.to(device, non_blocking=True)
+
+
+def _to_device_many(arrays: list[Tensor], device: torch.device) -> list[Tensor]:
+    """Several host tensors on the device in one asynchronous copy: packed
+    (16-byte aligned) into one fresh pinned block, copied on the current
+    stream, returned as typed views of the device copy (shapes kept).  Same
+    lifetime rules as ``_to_device``."""
+    if torch.device(device).type == "cpu":
+        return [a.clone() for a in arrays]
+    sizes = [a.numel() * a.element_size() for a in arrays]
+    offs, o = [], 0
+    for n in sizes:
+        offs.append(o)
+        o += (n + 15) // 16 * 16
+    staged = torch.empty(max(o, 16), dtype=torch.uint8, pin_memory=True)
+    for a, off, n in zip(arrays, offs, sizes):
+        if n:
+            staged[off:off + n].view(a.dtype).copy_(a.reshape(-1))
+    dev = staged.to(device, non_blocking=True)
+    return [dev[off:off + n].view(a.dtype).view(a.shape) for a, off, n in zip(arrays, offs, sizes)]
 
 
 def _build_cu_seqlens(seq_lens: list[int], device: torch.device) -> Tensor:
@@ -280,6 +301,7 @@ class WnWCache(FlatVarlenCache):
         L = self.num_layers
         self._pending_layer_events: list = [None] * L  # per layer: the copy of its loaded rows
         self._waited_groups: set = set()  # transfer-engine groups the compute stream already waits for
+        self._waited_events: set = set()  # (device-gather group event, stream) pairs already waited for
         self._pending_gpu_k: Tensor | None = None
         self._pending_gpu_v: Tensor | None = None
         self._pending_load_starts: list = [None] * L
@@ -607,14 +629,14 @@ class WnWCache(FlatVarlenCache):
         # gather waits only for the copy that used its pair two plans ago
         self._staging = [None, None]
         self._staging_turn = 0
-        # the offload channel (WNW_OFFLOAD): "device" (default), a gather
-        # kernel reading the pinned restore rows itself (the faster transfer:
-        # the CUs' reads of host memory outrun the copy engine, but they slow
-        # the compute kernels that run meanwhile); "copy", the transfer
-        # engine -- host gather threads and DMA copies per group of layers,
-        # which leave the compute kernels' memory traffic alone
+        # the offload channel (WNW_OFFLOAD): "copy" (default), the transfer
+        # engine -- host gather threads and DMA copies per group of layers
+        # on a side stream, which leave the compute kernels' memory traffic
+        # alone; "device", a gather kernel reading the pinned restore rows
+        # itself (its reads of host memory outrun the copy engine, but the
+        # compute kernels that run meanwhile slow down by more than that)
         self._load_groups = 8  # groups (copies + events) per plan: copy/compute overlap vs per-copy cost
-        mode = os.environ.get("WNW_OFFLOAD", "device")
+        mode = os.environ.get("WNW_OFFLOAD", "copy")
         if mode not in ("copy", "device"):
             raise ValueError(f"WNW_OFFLOAD must be 'copy' or 'device', got {mode!r}")
         if mode == "device" and self.cpu_restore_k.shape[0] > 0 and \
@@ -756,18 +778,26 @@ class WnWCache(FlatVarlenCache):
         self._ensure_headroom(l)
         nk = new_k.squeeze(2).reshape(-1, self.head_dim)
         nv = new_v.squeeze(2).reshape(-1, self.head_dim)
-        app = (nk, nv, self._cu_spare[l], self.seg_cap[l])
         rows = self._rows[l] + self.batch_size * self.num_kv_heads
         score_here = fused and self._layer_foldable[l]
+        # the cache's own tensors, checked when made: the launches skip the
+        # wrappers' argument checks (q and the new rows are the caller's and
+        # are checked here)
+        q_flat, nk, nv = q_flat.contiguous(), nk.contiguous(), nv.contiguous()
+        if not (q_flat.is_cuda and nk.is_cuda and nv.is_cuda and q_flat.dtype == nk.dtype == nv.dtype ==
+                self.layer_k[l].dtype and q_flat.shape[0] == nk.shape[0] == len(self.seq_lens[l])
+                and q_flat.shape[1:] == (self.num_q_heads // self.num_kv_heads, self.head_dim)):
+            raise _lib.WnwError("q and the new K/V rows must be GPU tensors of the cache's dtype, one per segment")
+        app = (nk, nv, self._cu_spare[l], self.seg_cap[l])
         if score_here:
             out = q1_decode_attn_score(q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale,
                                        self._ca_kv_mask_by_layer[l], self.num_kv_heads, self._decode_audio_starts_b,
                                        self._decode_audio_ends_b, self.score_accumulator, self.score_offsets,
                                        seg_base=self.seg_base[l], total_rows=rows, max_audio=self._max_audio,
-                                       append=app)
+                                       append=app, validate=False)
         else:
             out = decode_attn(q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale,
-                              seg_base=self.seg_base[l], total_rows=rows, append=app)
+                              seg_base=self.seg_base[l], total_rows=rows, append=app, validate=False)
         self._commit_append(l)
         if not score_here:
             self.decode_after_attn(l, q)
@@ -846,10 +876,11 @@ class WnWCache(FlatVarlenCache):
             self._clear_pending_rebuild_state()
             self._move_dev = None
 
-    def _plan_slack_moves(self, new_lens_all: list[list[int]]) -> None:
+    def _plan_slack_moves(self, new_lens_all: list[list[int]]) -> list[Tensor]:
         """Where a plan puts every layer's rows (slack layout), decided on the
-        host when the plan is made, with the device arrays sent in one copy
-        each for all layers.  In a layer the plan changes, every class-B
+        host when the plan is made; returns the host arrays of every layer's
+        move (bases, capacities, lengths, source lengths, offsets), which go
+        to the device with the plan's other descriptors.  In a layer the plan changes, every class-B
         segment (changed or not) is compacted with its loads into the half
         of the flip region the class-B segments do not occupy, packed with
         their slack; so the half they leave is wholly free for the next plan
@@ -875,10 +906,9 @@ class WnWCache(FlatVarlenCache):
             lens_all.append(lens)
             src_all.append(self.seq_lens[l])
             cu_all.append(_build_cu_seqlens_list(lens))
-        dev = self.device
-        self._move_dev = (_to_device(bases_all, torch.int64, dev), _to_device(caps_all, torch.int32, dev),
-                          _to_device(lens_all, torch.int32, dev), _to_device(src_all, torch.int32, dev),
-                          _to_device(cu_all, torch.int32, dev))
+        return [torch.tensor(bases_all, dtype=torch.int64), torch.tensor(caps_all, dtype=torch.int32),
+                torch.tensor(lens_all, dtype=torch.int32), torch.tensor(src_all, dtype=torch.int32),
+                torch.tensor(cu_all, dtype=torch.int32)]
 
     def _move_class_b(self, layer_idx: int, bases: list[int], caps: list[int], lens: list[int]) -> None:
         """The layer's class-B segments, compacted with their loads, into the
@@ -1003,13 +1033,14 @@ class WnWCache(FlatVarlenCache):
         else:
             self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
             self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
-        i32 = torch.int32
-        ls, ll, cun = (_to_device(o["load_starts_2d"], i32, dev), _to_device(o["load_lens_2d"], i32, dev),
-                       _to_device(o["cu_new_2d"], i32, dev))
-        eoff = _to_device(o["evict_offsets_2d"], i32, dev)
-        evs = _to_device(ev_s, i32, dev) if ev_s.numel() else self._empty_i32
-        eve = _to_device(ev_e, i32, dev) if ev_e.numel() else self._empty_i32
         elp, emax, new_lens = o["evict_layer_ptr"].tolist(), o["evict_max"].tolist(), o["new_lens_2d"].tolist()
+        # every descriptor of the plan (and of the slack layout's moves) in
+        # one host->device copy
+        host = [o["load_starts_2d"], o["load_lens_2d"], o["cu_new_2d"], o["evict_offsets_2d"], ev_s, ev_e]
+        moves = self._plan_slack_moves(new_lens) if self.slack_layout else []
+        devs = _to_device_many(host + moves, dev)
+        ls, ll, cun, eoff = (t.unbind(0) for t in devs[:4])
+        evs, eve = devs[4], devs[5]
         for l in range(self.num_layers):
             self._pending_load_starts[l], self._pending_load_lens[l], self._pending_cu_new[l] = ls[l], ll[l], cun[l]
             self._pending_evict_offsets[l] = eoff[l]
@@ -1018,9 +1049,9 @@ class WnWCache(FlatVarlenCache):
             lo, hi = elp[l], elp[l + 1]
             self._pending_evict_starts[l] = evs[lo:hi] if hi > lo else self._empty_i32
             self._pending_evict_ends[l] = eve[lo:hi] if hi > lo else self._empty_i32
+        if moves:
+            self._move_dev = tuple(t.unbind(0) for t in devs[6:])
         self._segments_changed_ranges = ranges
-        if self.slack_layout:
-            self._plan_slack_moves(new_lens)
         if total > 0 and self._record_plan_transfers and self.stats.enabled:
             # cache.py:816-820: host rows loaded per sample (K and V)
             per_row = self.head_dim * 2 * self.cpu_restore_k.element_size()
@@ -1046,8 +1077,7 @@ class WnWCache(FlatVarlenCache):
         stream = self._get_transfer_stream()
         events = [None] * self.num_layers
         with torch.cuda.stream(stream):
-            rg = _to_device(ranges, ranges.dtype, dev)
-            do = _to_device(dst, dst.dtype, dev)
+            rg, do = _to_device_many([ranges, dst], dev)
             pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
             pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
             r0 = 0
@@ -1063,6 +1093,7 @@ class WnWCache(FlatVarlenCache):
             t.record_stream(compute)
         self._pending_gpu_k, self._pending_gpu_v = pk, pv
         self._pending_layer_events = events
+        self._waited_events = set()  # these events are new (an id could repeat a dropped one's)
 
     def _layer_groups(self, ranges: Tensor, load_lens_2d: Tensor) -> tuple[list[int], list[int]]:
         """Groups of consecutive layers for a plan's loads: the range index
@@ -1185,8 +1216,11 @@ class WnWCache(FlatVarlenCache):
             if ev[1] not in self._waited_groups:
                 self._h2d.wait(ev[1], torch.cuda.current_stream(self.device))
                 self._waited_groups.add(ev[1])
-        else:
-            torch.cuda.current_stream(self.device).wait_event(ev)
+        else:  # a group's event: the stream waits once per group (its later work is ordered after)
+            key = (id(ev), _lib.stream_of(self.device).value)
+            if key not in self._waited_events:
+                torch.cuda.current_stream(self.device).wait_event(ev)
+                self._waited_events.add(key)
         self._pending_layer_events[layer_idx] = None
 
     def _finish_layer(self, layer_idx, k, v, cu_new, new_lens) -> None:
