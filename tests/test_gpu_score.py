@@ -193,6 +193,49 @@ def test_attn_score_bad_audio_range_is_flagged(keep_logits):
 
 
 @pytest.mark.parametrize("keep_logits", [True, False])
+def test_attn_score_short_accumulator_is_flagged(keep_logits):
+    """Offsets that put a sample's tokens past the accumulator's end set the
+    device error word; that sample writes nothing (not even past the end:
+    the accumulator is a view into a larger buffer whose tail must stay
+    untouched), the other sample is scored."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(15)
+    lens = [100, 50, 80, 60]  # B = 2, H = 2; KV head 0 is flagged
+    cu = cu_from_lens(lens)
+    q = to_torch(rand_rows(rng, 4 * 4, 64, "bfloat16").reshape(4, 4, 64), "bfloat16", dev)
+    k = to_torch(rand_rows(rng, int(cu[-1]), 64, "bfloat16"), "bfloat16", dev)
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)  # noqa: E731
+    big = torch.full((200,), 7.0, device=dev)
+    acc = big[:150]  # sample 1's 50 tokens would need [120, 170)
+    print(f"attn_score short accumulator keep_logits={keep_logits}", flush=True)
+    fused_attn.q1_decode_attn_score(q, k, k, t(cu), 0.125, t([1, 0]), 2, t([0, 0]), t([60, 50]), acc,
+                                    t([0, 120, 170]), max_audio=60, keep_logits=keep_logits)
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_BOUNDS
+    host = big.cpu()
+    assert float(host[:60].min()) > 7.0            # sample 0: scored
+    assert bool((host[60:] == 7.0).all())          # sample 1 refused; nothing past the end written
+    assert _lib.device_error() == 0
+
+
+def test_fused_score_negative_offset_is_flagged():
+    """A negative accumulator offset sets the device error word and writes nothing."""
+    dev = torch.device("cuda", 0)
+    q = torch.ones(2, 1, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.ones(64, 128, dtype=torch.bfloat16, device=dev)
+    big = torch.zeros(100, device=dev)
+    acc = big[10:]
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)  # noqa: E731
+    wk.fused_score_accumulate(q, k, t([0, 10]), t([10, 20]), t([0, 0]), t([5, 5]), acc, t([-5, 0, 5]))
+    torch.cuda.synchronize()
+    assert _lib.device_error() & _lib.DEVERR_BOUNDS
+    host = big.cpu()
+    assert float(host[:10].abs().sum()) == 0.0   # nothing before the accumulator
+    assert float(host[10:15].min()) > 0.0        # the valid item is scored
+    assert _lib.device_error() == 0
+
+
+@pytest.mark.parametrize("keep_logits", [True, False])
 def test_attn_score_many_samples(keep_logits):
     """Enough samples x audio rows for the long (16-iteration) scoring workgroups."""
     rng = np.random.default_rng(12)

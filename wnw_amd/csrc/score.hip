@@ -109,6 +109,10 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
   const int j0 = blockIdx.x * RPI * IT;
   if (j0 >= n_audio) return;  // workgroup-uniform
   const int64_t off = p.acc_off[b];
+  if (off < 0 || off + n_audio > p.acc_len) {  // the accumulator cannot hold this sample's tokens
+    if (tid == 0 && blockIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    return;  // workgroup-uniform
+  }
   float total[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) total[i] = 0.f;
@@ -119,7 +123,7 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
     if (s >= p.n_seg) break;
     const int64_t len = (int64_t)p.cu[s + 1] - p.cu[s];
     const int64_t base = p.base ? p.base[s] : (int64_t)p.cu[s];
-    if (a0 < 0 || a1 > len || base < 0 || base + len > p.kv_rows || off + n_audio > p.acc_len) {
+    if (a0 < 0 || a1 > len || base < 0 || base + len > p.kv_rows) {
       if (tid == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
       continue;  // uniform
     }
@@ -167,52 +171,110 @@ __global__ __launch_bounds__(kScoreThreads) void attn_score_kernel(AttnScorePara
 // sums the weights over the flagged KV heads and their query heads, and
 // adds the total to the accumulator once (no atomics).  The validity rules
 // are those of attn_score_kernel, so both passes score the same rows.
+// The fields of the first loads are the kernel's leading scalar arguments
+// (see logit_score_kernel); the rest come in this aggregate.
 struct LogitScoreParams {
   const float* xlog;       // [n_seg, G, max_audio]
-  const float* lse;        // [n_seg, G, 2] log2 domain
-  const int32_t* cu;       // [n_seg + 1]
-  const int64_t* base;     // [n_seg] or null
-  const int32_t* mask;     // [Hkv]
-  const int32_t* audio_s;  // [B]
-  const int32_t* audio_e;
   const int32_t* acc_off;  // [B + 1]
   float* acc;
   int32_t* err;
   int64_t kv_rows, acc_len, max_audio;
-  int32_t n_seg, G, Hkv;
 };
 
 static constexpr int kLogitThreads = 256;
+static constexpr int kLogitKv = 64;  // KV heads per sample this pass takes (a lane of wave 0 each)
+static constexpr int kLogitG = 8;    // query heads per KV head (the streaming kernel's limit)
 
-__global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(LogitScoreParams p) {
+// Latency, not bytes, bounds this pass (a few hundred KB per launch), so
+// its loads go out in two batches instead of a chain: wave 0 reads every
+// KV head's flag, bounds and normalisers at once (lane = KV head; the
+// sample's audio range and offset arrive in the same round trip) and lists
+// the flagged, valid segments in LDS; then every thread issues the loads
+// of all its logits and of its accumulator entry together.  Loads are
+// unconditional (indices clamped into range) and the checks combine with
+// bitwise operators, so no load waits behind a branch on another load.
+//
+// score.hip is built with 16 preloaded argument dwords, of which gfx950
+// delivers 14 in SGPRs at dispatch: the six tables of the first round trip
+// and the sizes their addresses need (hg = Hkv | G << 16, n_seg), so those
+// loads issue before any argument load returns.
+__global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(
+    const int32_t* audio_s, const int32_t* audio_e, const int32_t* mask, const int32_t* cu, const int64_t* seg_base,
+    const float* lse, int32_t hg, int32_t n_seg, LogitScoreParams p) {
+  __shared__ int32_t seg_sh[kLogitKv];
+  __shared__ float m_sh[kLogitKv * kLogitG], inv_sh[kLogitKv * kLogitG];
+  __shared__ int32_t n_sh;
   const int b = blockIdx.y;
-  const int a0 = p.audio_s[b], a1 = p.audio_e[b];
-  const int n_audio = a1 - a0;
-  const int64_t j = (int64_t)blockIdx.x * kLogitThreads + threadIdx.x;
-  if ((int64_t)blockIdx.x * kLogitThreads >= min((int64_t)n_audio, p.max_audio)) return;  // uniform
-  const bool valid = j < n_audio && j < p.max_audio;
-  const int64_t off = p.acc_off[b];
-  float total = 0.f;
-  for (int kv = 0; kv < p.Hkv; ++kv) {
-    if (!p.mask[kv]) continue;
-    const int s = b * p.Hkv + kv;
-    if (s >= p.n_seg) break;
-    const int64_t len = (int64_t)p.cu[s + 1] - p.cu[s];
-    const int64_t base = p.base ? p.base[s] : (int64_t)p.cu[s];
-    if (a0 < 0 || a1 > len || base < 0 || base + len > p.kv_rows || off + n_audio > p.acc_len) {
-      if (threadIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
-      continue;  // uniform
+  const int tid = threadIdx.x;
+  const int Hkv = hg & 0xffff, G = hg >> 16;
+  const int a0 = audio_s[b], a1 = audio_e[b];
+  if (tid < 64) {  // wave 0
+    const int kv = min(tid, Hkv - 1);
+    const int s = min(b * Hkv + kv, n_seg - 1);
+    const int32_t flag = mask[kv];
+    const int64_t bv = seg_base ? seg_base[s] : 0;
+    const int64_t c0 = cu[s], c1 = cu[s + 1];
+    float m[kLogitG], l[kLogitG];
+#pragma unroll
+    for (int g = 0; g < kLogitG; ++g) {
+      const int64_t e = ((int64_t)s * G + min(g, G - 1)) * 2;
+      m[g] = lse[e];
+      l[g] = lse[e + 1];
     }
-    float sc = 0.f;
-    for (int g = 0; g < p.G; ++g) {
-      const float m = p.lse[((int64_t)s * p.G + g) * 2];
-      const float inv = 1.f / p.lse[((int64_t)s * p.G + g) * 2 + 1];
-      const float x = valid ? p.xlog[((int64_t)s * p.G + g) * p.max_audio + j] : m;
-      sc += exp2f(x - m) * inv;
+    const int64_t len = c1 - c0;
+    const int64_t base = seg_base ? bv : c0;
+    const bool flagged = (tid < Hkv) & (b * Hkv + tid < n_seg) & (flag != 0);
+    const bool oob = (a0 < 0) | (a1 > len) | (base < 0) | (base + len > p.kv_rows);
+    const bool use = flagged & !oob;
+    if (flagged & oob & (blockIdx.x == 0)) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    const uint64_t bal = __ballot(use);
+    if (use) {
+      const int pos = __popcll(bal & ((1ull << tid) - 1ull));
+      seg_sh[pos] = s;
+#pragma unroll
+      for (int g = 0; g < kLogitG; ++g) {
+        m_sh[pos * kLogitG + g] = m[g];
+        inv_sh[pos * kLogitG + g] = 1.f / l[g];
+      }
     }
-    total += sc;
+    if (tid == 0) n_sh = __popcll(bal);
   }
-  if (valid) p.acc[off + j] += total;
+  const int64_t off = p.acc_off[b];
+  const int n_audio = a1 - a0;
+  if ((int64_t)blockIdx.x * kLogitThreads >= min((int64_t)n_audio, p.max_audio)) return;  // uniform
+  if (off < 0 || off + n_audio > p.acc_len) {  // the accumulator cannot hold this sample's tokens
+    if (tid == 0 && blockIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    return;  // uniform
+  }
+  __syncthreads();
+  const int64_t j = (int64_t)blockIdx.x * kLogitThreads + tid;
+  const bool valid = j < n_audio && j < p.max_audio;
+  const int64_t jc = valid ? j : 0;  // loads stay unconditional; `valid` gates the store
+  const float prior = p.acc[off + jc];
+  const int nt = n_sh * G;
+  float total = 0.f, sc = 0.f;  // a segment's heads are summed first, then added to the total
+  for (int t0 = 0; t0 < nt; t0 += 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = min(t0 + u, nt - 1);
+      const int i = t / G, g = t - i * G;
+      x[u] = p.xlog[((int64_t)seg_sh[i] * G + g) * p.max_audio + jc];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + u;
+      if (t < nt) {
+        const int i = t / G, g = t - i * G;
+        sc += exp2f(x[u] - m_sh[i * kLogitG + g]) * inv_sh[i * kLogitG + g];
+        if (g == G - 1) {
+          total += sc;
+          sc = 0.f;
+        }
+      }
+    }
+  }
+  if (valid) p.acc[off + j] = prior + total;
 }
 
 // ---------------------------------------------------------------------------
@@ -322,7 +384,7 @@ __global__ __launch_bounds__(kScoreThreads) void seg_score_kernel(SegScoreParams
   const int j0 = blockIdx.x * RPI * IT;
   if (j0 >= n_audio) return;
   const int64_t off = p.acc_off[s];
-  if (r0 < 0 || r1 < r0 || r1 > p.k_rows || a0 < 0 || r0 + a1 > r1 || off + n_audio > p.acc_len) {
+  if (r0 < 0 || r1 < r0 || r1 > p.k_rows || a0 < 0 || r0 + a1 > r1 || off < 0 || off + n_audio > p.acc_len) {
     if (tid == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
     return;
   }
@@ -455,7 +517,8 @@ static int decode_attn_score_impl(const void* q, const void* k, const void* v, c
   lg.audio_e = audio_ends;
   lg.max_audio = max_audio;
   lg.hkv = (int32_t)num_kv_heads;
-  const bool room = max_audio > 0 && workspace_bytes >= xoff + n_seg * group * max_audio * 4;
+  const bool room = max_audio > 0 && num_kv_heads <= kLogitKv && group <= kLogitG &&
+                    workspace_bytes >= xoff + n_seg * group * max_audio * 4;
   int kept = 0;
   int rc = decode_attn_impl(q, k, v, cu_k, seg_base, n_seg, group, head_dim, total_rows, kv_rows, scale,
                             dtype, out, workspace, attn_ws, WNW_ATTN_AUTO, 0, lse, room ? &lg : nullptr, &kept,
@@ -465,23 +528,16 @@ static int decode_attn_score_impl(const void* q, const void* k, const void* v, c
   if (kept) {
     LogitScoreParams lp;
     lp.xlog = lg.xlog;
-    lp.lse = lse;
-    lp.cu = cu_scored;
-    lp.base = seg_base;
-    lp.mask = ca_kv_mask;
-    lp.audio_s = audio_starts;
-    lp.audio_e = audio_ends;
     lp.acc_off = score_offsets;
     lp.acc = score_acc;
     lp.err = device_error_word();
     lp.kv_rows = kv_rows;
     lp.acc_len = acc_len;
     lp.max_audio = max_audio;
-    lp.n_seg = (int32_t)n_seg;
-    lp.G = (int32_t)group;
-    lp.Hkv = (int32_t)num_kv_heads;
+    const int32_t hg = (int32_t)num_kv_heads | ((int32_t)group << 16);  // room: Hkv <= 64, G <= 8
     const dim3 grid((unsigned)((max_audio + kLogitThreads - 1) / kLogitThreads), (unsigned)(n_seg / num_kv_heads));
-    hipLaunchKernelGGL(logit_score_kernel, grid, dim3(kLogitThreads), 0, (hipStream_t)stream, lp);
+    hipLaunchKernelGGL(logit_score_kernel, grid, dim3(kLogitThreads), 0, (hipStream_t)stream, audio_starts,
+                       audio_ends, ca_kv_mask, cu_scored, seg_base, (const float*)lse, hg, (int32_t)n_seg, lp);
     WNW_CHECK_HIP(hipGetLastError(), "logit score launch");
     return WNW_OK;
   }
