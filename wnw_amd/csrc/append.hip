@@ -428,6 +428,7 @@ extern "C" int wnw_append_inplace(void* k_pool, void* v_pool, const void* new_k,
                 "rows must be 16-byte aligned");
   const int64_t nthreads = std::max<int64_t>(n_seg * cpr, n_seg + 1);
   const int64_t blocks = (nthreads + kNT - 1) / kNT;
+  WNW_CHECK_ARG(blocks < (1ll << 31), "too many rows");
   hipLaunchKernelGGL(append_inplace_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream,
                      (u32x4*)k_pool, (u32x4*)v_pool, (const u32x4*)new_k, (const u32x4*)new_v, cu_old,
                      cu_new, seg_base, seg_cap, (int)n_seg, pool_rows, cpr, device_error_word());
