@@ -213,6 +213,60 @@ def test_decreasing_offsets_leave_workspace_valid(gpu, kernel, n_seg):
     assert ok, msg
 
 
+def test_repeated_launches_reuse_workspace(gpu):
+    """Counters are left at zero: many launches with different shapes stay correct."""
+    for i, lens in enumerate([[300, 5000, 12], [7, 7, 7, 7, 7000], [1, 2, 3], [6000, 6000]]):
+        got, ref = _run_case(gpu, lens, 4, 128, "bfloat16", seed=20 + i)
+        ok, msg = allclose_report(got, ref, ATOL, RTOL)
+        assert ok, msg
+
+
+def test_cfg1_fp32_and_bf16(gpu):
+    """Config 1 (fp32 plumbing) through the VALU kernel, and its bf16 cast through MFMA."""
+    cfg = workloads.config1()
+    lens = cfg.lengths[0] + 1
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "float32", seed=0)
+    ok, msg = allclose_report(got, ref, 1e-4, 1e-3)
+    assert ok, msg
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=0)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("name,layer", [("cfg2", 0), ("cfg3", 0), ("cfg5", 0)])
+def test_config_layer_full_size(gpu, name, layer):
+    """One full-size layer of configs 2, 3 and 5 against the float64 oracle."""
+    cfg = workloads.CONFIGS[name]()
+    lens = cfg.lengths[layer] + 1
+    kvs = float(cfg.kv_scale[layer].mean())
+    got, ref = _run_case(gpu, lens, cfg.group, cfg.head_dim, "bfloat16", seed=layer, kv_scale=kvs)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    print(name, msg)
+    assert ok, msg
+
+
+def test_large_scores_are_stable(gpu):
+    """Keys scaled x8: scores up to ~+-100 must not overflow the online softmax."""
+    got, ref = _run_case(gpu, [2000, 33, 517], 4, 128, "bfloat16", seed=30, kv_scale=8.0)
+    ok, msg = allclose_report(got, ref, ATOL, RTOL)
+    assert ok, msg
+
+
+def test_q1_decode_attn_reference_signature(gpu):
+    rng = np.random.default_rng(31)
+    lens = [100, 3000, 7]
+    cu = cu_from_lens(lens)
+    q = rand_rows(rng, 3 * 4, 128, "bfloat16").reshape(3, 4, 128)
+    k = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
+    v = rand_rows(rng, int(cu[-1]), 128, "bfloat16")
+    ref = oracle.decode_attn(q, k, v, cu, 0.1, dtype=oracle.DT_BF16)
+    out = fused_attn.q1_decode_attn(to_torch(q, "bfloat16", gpu), to_torch(k, "bfloat16", gpu),
+                                    to_torch(v, "bfloat16", gpu), torch.from_numpy(cu).to(gpu), 0.1)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (3, 4, 128)
+    ok, msg = allclose_report(oracle.to_f64(from_torch(out, "bfloat16"), oracle.DT_BF16), ref, ATOL, RTOL)
+    assert ok, msg
+
+
 def test_bad_offsets_are_refused_not_read(gpu):
     """A segment pointing past the K/V rows sets the device error word instead of faulting."""
     n, G, D = 2, 4, 128
