@@ -406,7 +406,10 @@ int wnw_chunk_topk(const float* score_acc, int64_t acc_len,
  * only until that copy is issued); wnw_h2d_join waits until every group is
  * issued.  Staging is used in two alternating pairs by the caller: a start
  * waits for the copies of the start before the previous one (the last use
- * of its pair) before gathering.  At most 64 groups.
+ * of its pair) before gathering.  At most 64 groups.  After a HIP error the
+ * job's remaining groups are not gathered, their waits return the error, and
+ * the engine drains the stream.  wnw_h2d_destroy returns once every issued
+ * copy has finished, so the caller may then free the staging.
  */
 typedef struct wnw_h2d wnw_h2d;
 wnw_h2d* wnw_h2d_create(int n_workers);  /* NULL on error */

@@ -74,7 +74,9 @@ struct wnw_h2d {
   int task_group = -1;
   int task_done = 0;
   hipEvent_t events[2][kMaxGroups] = {};
-  int last_groups[2] = {0, 0};  // groups of the last job of each parity (0: none yet)
+  // events recorded by the last job of each parity (0: none to wait for);
+  // the last of them follows every copy that job issued
+  int last_groups[2] = {0, 0};
   int parity = 0;
   int n_workers = 0;
 };
@@ -130,8 +132,9 @@ void lead_loop(wnw_h2d* x) {
     // (the events record in stream order, so the last one covers them all)
     if (e == hipSuccess && x->last_groups[j.parity] > 0)
       e = hipEventSynchronize(x->events[j.parity][x->last_groups[j.parity] - 1]);
+    int recorded = 0;
     for (int g = 0; g < x->groups; ++g) {
-      {
+      if (e == hipSuccess) {  // after an error the staging is left alone (copies may still read it)
         std::unique_lock<std::mutex> lk(x->mu);
         x->task_group = g;
         x->task_done = 0;
@@ -148,6 +151,7 @@ void lead_loop(wnw_h2d* x) {
         e = hipMemcpyAsync(j.dev_v + d0 * j.row_bytes, j.stg_v + d0 * j.row_bytes, bytes, hipMemcpyHostToDevice,
                            j.stream);
       if (e == hipSuccess) e = hipEventRecord(x->events[j.parity][g], j.stream);
+      if (e == hipSuccess) recorded = g + 1;
       {
         std::lock_guard<std::mutex> lk(x->mu);
         if (e != hipSuccess && x->error == WNW_OK) {
@@ -158,9 +162,15 @@ void lead_loop(wnw_h2d* x) {
         x->cv_issued.notify_all();
       }
     }
+    // after an error some copy may have no event after it: drain the stream,
+    // so the next job of this parity has nothing to wait for
+    if (recorded < x->groups) {
+      (void)hipStreamSynchronize(j.stream);
+      recorded = 0;
+    }
     {
       std::lock_guard<std::mutex> lk(x->mu);
-      x->last_groups[j.parity] = x->groups;
+      x->last_groups[j.parity] = recorded;
       x->job_running = false;
       x->cv_issued.notify_all();
     }
@@ -208,6 +218,10 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
   x->cv_task.notify_all();
   x->lead.join();
   for (auto& t : x->workers) t.join();
+  // the caller may free the staging once this returns: the issued copies
+  // that read it end first
+  for (int p = 0; p < 2; ++p)
+    if (x->last_groups[p] > 0) (void)hipEventSynchronize(x->events[p][x->last_groups[p] - 1]);
   for (int p = 0; p < 2; ++p)
     for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->events[p][g]);
   delete x;
