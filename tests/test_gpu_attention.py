@@ -94,8 +94,15 @@ def test_more_workgroups_than_rows(gpu):
 
 
 def test_all_segments_empty(gpu):
+    """Segments with no rows return zeros, as flash-style varlen kernels (the
+    reference's default `varlen_attn`, session.py:101-106) do for an empty
+    key range.  This departs from the reference's Triton q1_decode_attn,
+    which divides 0 by 0 there (src/common/kv/fused_attn.py:42, o = acc / l
+    with l = 0) and returns NaN; the cache never makes an empty segment
+    (every segment holds at least the step's own row)."""
     got, ref = _run_case(gpu, [0, 0, 0], 4, 128, "bfloat16", seed=7)
     assert np.all(got == 0)
+    np.testing.assert_array_equal(ref, 0.0)  # the oracle keeps the same rule
 
 
 def test_single_row_returns_v_exactly(gpu):
