@@ -125,13 +125,18 @@ def ptr(t: torch.Tensor | None):
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def stream_of(device: torch.device) -> ctypes.c_void_p:
-    """The current HIP stream of ``device`` (the raw handle, without building
-    a torch Stream object where torch offers that)."""
+def raw_stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle, without
+    building a torch Stream object where torch offers that."""
     if _raw_stream is not None:
         idx = device.index if device.index is not None else torch.cuda.current_device()
-        return ctypes.c_void_p(_raw_stream(idx))
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        return int(_raw_stream(idx))
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def stream_of(device: torch.device) -> ctypes.c_void_p:
+    """The current HIP stream of ``device`` (the raw handle)."""
+    return ctypes.c_void_p(raw_stream(device))
 
 
 def require_gpu(*tensors: torch.Tensor) -> None:

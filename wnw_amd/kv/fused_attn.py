@@ -63,7 +63,7 @@ _workspaces: dict[tuple[int, int], AttnWorkspace] = {}
 
 def workspace_for(device: torch.device) -> AttnWorkspace:
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(device).cuda_stream)
+    key = (idx, _lib.raw_stream(device))
     ws = _workspaces.get(key)
     if ws is None:
         ws = AttnWorkspace(torch.device("cuda", idx))

@@ -776,8 +776,8 @@ class WnWCache(FlatVarlenCache):
         self._before_decode_layer(l)
         self._apply_pending_slack(l)
         self._ensure_headroom(l)
-        nk = new_k.squeeze(2).reshape(-1, self.head_dim)
-        nv = new_v.squeeze(2).reshape(-1, self.head_dim)
+        nk = new_k.reshape(-1, self.head_dim)  # [B, Hkv, 1, D] -> [N, D]
+        nv = new_v.reshape(-1, self.head_dim)
         rows = self._rows[l] + self.batch_size * self.num_kv_heads
         score_here = fused and self._layer_foldable[l]
         # the cache's own tensors, checked when made: the launches skip the

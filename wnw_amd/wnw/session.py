@@ -49,7 +49,8 @@ def decode_attention(cache, layer_idx: int, q: Tensor, k: Tensor, v: Tensor, sca
     B = q.shape[0]
     H, G, D = cache.num_kv_heads, cache.num_kv_groups, cache.head_dim
     cache.update(k, v, layer_idx)
-    q_flat = q.squeeze(2).reshape(B, H, G, D).reshape(B * H, G, D)
+    # [B, H*G, 1, D] -> [B*H, G, D]: one view when q is contiguous
+    q_flat = q.view(B * H, G, D) if q.is_contiguous() else q.squeeze(2).reshape(B * H, G, D)
     step = getattr(cache, "decode_step_attention", None)
     if step is not None:
         # the WnW cache appends and attends in one launch (slack layout)
@@ -61,7 +62,7 @@ def decode_attention(cache, layer_idx: int, q: Tensor, k: Tensor, v: Tensor, sca
         else:
             out = q1_decode_attn(q_flat, k_flat, v_flat, cu_k, scaling)
             cache.decode_after_attn(layer_idx, q)
-    out = out.reshape(B, H * G, D).unsqueeze(1).reshape(B, 1, H * G * D)
+    out = out.reshape(B, 1, H * G * D)  # [B*H, G, D] -> [B, 1, Hq*D] (q head = kv*G + g)
     if layer_idx == cache.num_layers - 1:
         cache.decode_all_layers_done()
     return out
