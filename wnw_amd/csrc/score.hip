@@ -502,6 +502,7 @@ static int decode_attn_score_impl(const void* q, const void* k, const void* v, c
   WNW_CHECK_ARG(ca_kv_mask && audio_starts && audio_ends && score_acc && score_offsets,
                 "null pointer argument");
   WNW_CHECK_ARG(max_audio >= 0 && acc_len >= 0, "negative max_audio / acc_len");
+  WNW_CHECK_ARG(n_seg / num_kv_heads <= 65535, "at most 65535 samples (the scoring grid's y extent)");
   const int64_t attn_ws = wnw_decode_attn_workspace_bytes(n_seg, group, head_dim);
   WNW_CHECK_ARG(attn_ws >= 0 && workspace_bytes >= attn_ws + up256(n_seg * group * 8),
                 "workspace too small for attention + normalisers");
