@@ -327,6 +327,11 @@ def main():
                               f"(profiles/decode_attn_{cfg.name}_traffic.json)"},
         "cpu_baseline": cpu,
     }
+    rl = line["roofline"]
+    if rl is not None and rl["traffic"]:
+        # measured HBM bytes per launch over the same launch time (the
+        # counter-based rate beside the algorithmic one)
+        rl["traffic_GBs"] = round(rl["traffic"] / (fused_us * 1e-6) / 1e9, 1)
     print(json.dumps(line), flush=True)
 
 
