@@ -66,7 +66,7 @@ def parse():
     ap.add_argument("--cpu-sample-layers", type=int, default=0,
                     help="layers timed for the CPU baseline (0 = choose ~15 s of work)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-compaction", action="store_true", help="skip the compaction timing")
+    ap.add_argument("--no-compaction", action="store_true", help="skip the compaction and append timings")
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy three times (PMC byte calibration)")
@@ -304,6 +304,7 @@ def main():
         attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
 
     compact = None if args.no_compaction else compaction_timing(cfg, cache, inputs, dev)
+    append_t = None if args.no_compaction else append_timing(cfg, cache, inputs, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, cache, inputs, scale, args.cpu_sample_layers)
     line = {
         "metric": METRIC, "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps,
@@ -319,6 +320,7 @@ def main():
         "attn_only_us_per_layer_step": None if attn_us is None else round(attn_us, 3),
         "attn_only_TBs": None if attn_gbs is None else round(attn_gbs / 1e3, 4),
         "compaction": compact,
+        "append": append_t,
         "roofline": None if achieved is None else {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name),
@@ -393,6 +395,59 @@ def compaction_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
             "TBs": round(bytes_per_launch / (us * 1e-6) / 1e12, 3),
             "frac_of_peak": round(bytes_per_launch / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "workload": "dense layout, class-B segments drop row 4 (evict [4, 5)), one new row per segment"}
+
+
+def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
+    """The reference's out-of-place append (``interleave_append``, twice per
+    layer: K and V) on the dense layout: every row read and written once
+    more, plus the step's new rows.  Bytes = (T + N rows read + T + N rows
+    written) x 2 tensors.  (The cache's own path fuses the append into the
+    attention launch; this times the standalone operator of row a3.)"""
+    import numpy as np
+    import torch
+
+    from wnw_amd.kv.kernels import interleave_append
+
+    D, N = cfg.head_dim, cfg.n_seg
+    calls, moved = [], 0
+    for li in range(cfg.layers):
+        dk, dv = cache.dense_kv(li)
+        lens = np.asarray(cache.seq_lens[li], np.int64)
+        cu_old = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        cu_new = cu_old + np.arange(N + 1, dtype=np.int32)
+        nk = inputs[li][1].reshape(N, D)
+        nv = inputs[li][2].reshape(N, D)
+        calls.append((dk, dv, nk, nv, torch.from_numpy(cu_old).to(dev), torch.from_numpy(cu_new).to(dev)))
+        T = int(cu_old[-1])
+        moved += (T + N) * D * 2 * 2 * 2  # read and written, K and V
+    torch.cuda.synchronize()
+
+    def launches():
+        for dk, dv, nk, nv, co, cn in calls:
+            interleave_append(dk, nk, co, cn)
+            interleave_append(dv, nv, co, cn)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        launches()  # allocates the outputs before capture
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            launches()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        graph.replay()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * cfg.layers)
+    bytes_per_layer = moved / cfg.layers
+    return {"kernel": "interleave_append_kernel (K and V)", "us_per_layer_step": round(us, 3),
+            "bytes_per_layer_step": int(bytes_per_layer),
+            "TBs": round(bytes_per_layer / (us * 1e-6) / 1e12, 3),
+            "frac_of_peak": round(bytes_per_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "workload": "dense layout, one new row per segment, out of place (the reference operator)"}
 
 
 def traffic_from_profiles(workload: str):
