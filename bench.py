@@ -398,15 +398,16 @@ def compaction_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
 
 
 def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
-    """The reference's out-of-place append (``interleave_append``, twice per
-    layer: K and V) on the dense layout: every row read and written once
-    more, plus the step's new rows.  Bytes = (T + N rows read + T + N rows
-    written) x 2 tensors.  (The cache's own path fuses the append into the
-    attention launch; this times the standalone operator of row a3.)"""
+    """The out-of-place append of the dense layout (the reference's
+    ``interleave_append`` of K and V, here one launch for both tensors,
+    ``interleave_append_kv``, as the cache's dense path calls it): every row
+    read and written once more, plus the step's new rows.  Bytes = (T + N
+    rows read + T + N rows written) x 2 tensors.  (The cache's default slack
+    layout fuses its append into the attention launch instead.)"""
     import numpy as np
     import torch
 
-    from wnw_amd.kv.kernels import interleave_append
+    from wnw_amd.kv.kernels import interleave_append_kv
 
     D, N = cfg.head_dim, cfg.n_seg
     calls, moved = [], 0
@@ -424,8 +425,7 @@ def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
 
     def launches():
         for dk, dv, nk, nv, co, cn in calls:
-            interleave_append(dk, nk, co, cn)
-            interleave_append(dv, nv, co, cn)
+            interleave_append_kv(dk, dv, nk, nv, co, cn)
 
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
@@ -443,11 +443,11 @@ def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
         e1.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (reps * cfg.layers)
     bytes_per_layer = moved / cfg.layers
-    return {"kernel": "interleave_append_kernel (K and V)", "us_per_layer_step": round(us, 3),
+    return {"kernel": "interleave_append_kernel<true> (K and V, one launch)", "us_per_layer_step": round(us, 3),
             "bytes_per_layer_step": int(bytes_per_layer),
             "TBs": round(bytes_per_layer / (us * 1e-6) / 1e12, 3),
             "frac_of_peak": round(bytes_per_layer / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "workload": "dense layout, one new row per segment, out of place (the reference operator)"}
+            "workload": "dense layout, one new row per segment, out of place (the reference operator's semantics)"}
 
 
 def traffic_from_profiles(workload: str):

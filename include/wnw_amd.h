@@ -95,6 +95,19 @@ int wnw_interleave_append(const void* old_rows, const void* new_rows,
                           int dtype, void* out, void* stream);
 
 /*
+ * wnw_interleave_append of K and V in one launch: the pair of calls
+ * decode_before_attn makes (src/algorithms/wnw/code/cache.py:506-507, each
+ * the reference's interleave_append, src/common/kv/kernels.py:45-73), with
+ * every row's source resolved once for both tensors.  out_k / out_v as
+ * wnw_interleave_append's out.
+ */
+int wnw_interleave_append_kv(const void* old_k, const void* old_v,
+                             const void* new_k, const void* new_v,
+                             const int32_t* cu_old, const int32_t* cu_new,
+                             int64_t n_seg, int64_t total_old, int64_t head_dim,
+                             int dtype, void* out_k, void* out_v, void* stream);
+
+/*
  * In-place append into a layout with per-segment slack (no reference
  * counterpart; it replaces the two full-layer copies of
  * src/algorithms/wnw/code/cache.py:506-507 for caches that keep slack).

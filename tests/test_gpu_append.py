@@ -35,6 +35,31 @@ def test_interleave_append_bit_exact(gpu, dtype, D, n_seg):
     np.testing.assert_array_equal(from_torch(out, dtype), ref)
 
 
+@pytest.mark.parametrize("dtype,D", [("bfloat16", 128), ("float32", 128), ("float16", 64)])
+@pytest.mark.parametrize("n_seg", [1, 64, 1500])
+def test_interleave_append_kv_bit_exact(gpu, dtype, D, n_seg):
+    """K and V appended in one launch: each bit-exact against the oracle's
+    interleave_append of that tensor (the reference's two calls)."""
+    rng = np.random.default_rng(7 * n_seg + D)
+    lens = rng.integers(0, 300, size=n_seg)
+    lens[rng.random(n_seg) < 0.1] = 0
+    cu_old = cu_from_lens(lens)
+    cu_new = cu_old + np.arange(n_seg + 1, dtype=np.int32)
+    ok_, ov_ = rand_rows(rng, int(cu_old[-1]), D, dtype), rand_rows(rng, int(cu_old[-1]), D, dtype)
+    nk, nv = rand_rows(rng, n_seg, D, dtype), rand_rows(rng, n_seg, D, dtype)
+    print(f"interleave_append_kv n_seg={n_seg} rows={cu_old[-1]} {dtype} D={D}", flush=True)
+    code = DTYPE_CODES[dtype]
+    rk = oracle.interleave_append(ok_, nk, cu_old, cu_new, dtype=code)
+    rv = oracle.interleave_append(ov_, nv, cu_old, cu_new, dtype=code)
+    gk, gv = kv_kernels.interleave_append_kv(to_torch(ok_, dtype, gpu), to_torch(ov_, dtype, gpu),
+                                             to_torch(nk, dtype, gpu), to_torch(nv, dtype, gpu), _t(cu_old, gpu),
+                                             _t(cu_new, gpu))
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    np.testing.assert_array_equal(from_torch(gk, dtype), rk)
+    np.testing.assert_array_equal(from_torch(gv, dtype), rv)
+
+
 @pytest.mark.parametrize("seed", range(4))
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_rebuild_append_kv_bit_exact(gpu, seed, dtype):

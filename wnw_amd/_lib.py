@@ -33,6 +33,7 @@ _SIGNATURES = {
     "wnw_init": (_i32, []),
     "wnw_device_error": (_i32, [_i32]),
     "wnw_interleave_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
+    "wnw_interleave_append_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "wnw_append_inplace": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "wnw_rebuild_append_kv": (_i32, [_vp] * 13 + [_i64] * 7 + [_i32, _vp, _vp, _vp]),
     "wnw_compact_segments": (_i32, [_vp] * 9 + [_i64, _i64, _i64] + [_vp] * 9 + [_i64, _i32, _i64, _i64, _i64,

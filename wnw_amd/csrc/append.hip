@@ -151,10 +151,15 @@ __device__ __forceinline__ void copy_rows(const RowSrc& rs, int nrows, int cpr, 
 // ---------------------------------------------------------------------------
 // interleave_append (reference src/common/kv/kernels.py:7-73)
 // ---------------------------------------------------------------------------
+// KV: K and V appended in one launch (the rows' sources are resolved once
+// for both tensors, as in the rebuild kernel).
+template <bool KV>
 __global__ __launch_bounds__(kNT) void interleave_append_kernel(
     const u32x4* __restrict__ old_rows, const u32x4* __restrict__ new_rows,
     const int32_t* __restrict__ cu_old, const int32_t* __restrict__ cu_new, int N,
-    int64_t total_old, int64_t total_out, int cpr, u32x4* __restrict__ out, int32_t* err) {
+    int64_t total_old, int64_t total_out, int cpr, u32x4* __restrict__ out, int32_t* err,
+    const u32x4* __restrict__ old_v = nullptr, const u32x4* __restrict__ new_v = nullptr,
+    u32x4* __restrict__ out_v = nullptr) {
   __shared__ BlockSegs bs;
   __shared__ RowSrc rs;
   const int64_t B0 = (int64_t)blockIdx.x * kRows;
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(kNT) void interleave_append_kernel(
     rs.row[threadIdx.x] = src;
   }
   __syncthreads();
-  copy_rows<false>(rs, nrows, cpr, old_rows, nullptr, nullptr, nullptr, new_rows, nullptr, B0, out, nullptr);
+  copy_rows<KV>(rs, nrows, cpr, old_rows, old_v, nullptr, nullptr, new_rows, new_v, B0, out, out_v);
 }
 
 // ---------------------------------------------------------------------------
@@ -407,10 +412,33 @@ extern "C" int wnw_interleave_append(const void* old_rows, const void* new_rows,
   WNW_CHECK_ARG(aligned16(old_rows) && aligned16(new_rows) && aligned16(out), "rows must be 16-byte aligned");
   const int64_t blocks = (total_out + kRows - 1) / kRows;
   WNW_CHECK_ARG(blocks < (1ll << 31), "too many rows");
-  hipLaunchKernelGGL(interleave_append_kernel, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream, (const u32x4*)old_rows,
-                     (const u32x4*)new_rows, cu_old, cu_new, (int)n_seg, total_old, total_out, cpr, (u32x4*)out,
-                     device_error_word());
+  hipLaunchKernelGGL(interleave_append_kernel<false>, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream,
+                     (const u32x4*)old_rows, (const u32x4*)new_rows, cu_old, cu_new, (int)n_seg, total_old, total_out,
+                     cpr, (u32x4*)out, device_error_word(), nullptr, nullptr, nullptr);
   WNW_CHECK_HIP(hipGetLastError(), "interleave_append launch");
+  return WNW_OK;
+}
+
+extern "C" int wnw_interleave_append_kv(const void* old_k, const void* old_v, const void* new_k, const void* new_v,
+                                        const int32_t* cu_old, const int32_t* cu_new, int64_t n_seg,
+                                        int64_t total_old, int64_t head_dim, int dtype, void* out_k, void* out_v,
+                                        void* stream) {
+  int cpr = 0;
+  if (int rc = check_rows(head_dim, dtype, cpr)) return rc;
+  WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1 << 30) && total_old >= 0, "bad sizes");
+  const int64_t total_out = total_old + n_seg;
+  if (total_out == 0) return WNW_OK;
+  WNW_CHECK_ARG(new_k && new_v && cu_old && cu_new && out_k && out_v && ((old_k && old_v) || total_old == 0),
+                "null pointer argument");
+  WNW_CHECK_ARG(aligned16(old_k) && aligned16(old_v) && aligned16(new_k) && aligned16(new_v) && aligned16(out_k) &&
+                    aligned16(out_v),
+                "rows must be 16-byte aligned");
+  const int64_t blocks = (total_out + kRows - 1) / kRows;
+  WNW_CHECK_ARG(blocks < (1ll << 31), "too many rows");
+  hipLaunchKernelGGL(interleave_append_kernel<true>, dim3((unsigned)blocks), dim3(kNT), 0, (hipStream_t)stream,
+                     (const u32x4*)old_k, (const u32x4*)new_k, cu_old, cu_new, (int)n_seg, total_old, total_out, cpr,
+                     (u32x4*)out_k, device_error_word(), (const u32x4*)old_v, (const u32x4*)new_v, (u32x4*)out_v);
+  WNW_CHECK_HIP(hipGetLastError(), "interleave_append_kv launch");
   return WNW_OK;
 }
 

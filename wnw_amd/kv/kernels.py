@@ -52,6 +52,42 @@ def interleave_append(
     return out
 
 
+
+def interleave_append_kv(
+    old_k: torch.Tensor,
+    old_v: torch.Tensor,
+    new_k: torch.Tensor,
+    new_v: torch.Tensor,
+    cu_old: torch.Tensor,
+    cu_new: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``interleave_append`` of K and V in one launch (the two calls of
+    decode_before_attn, src/algorithms/wnw/code/cache.py:506-507); each
+    result is bit-identical to ``interleave_append`` of that tensor."""
+    _lib.require_gpu(old_k, old_v, new_k, new_v, cu_old, cu_new)
+    if old_k.shape != old_v.shape or new_k.shape != new_v.shape or old_k.dim() != 2 or new_k.dim() != 2 or \
+            old_k.shape[1] != new_k.shape[1]:
+        raise _lib.WnwError(f"shape mismatch: old {tuple(old_k.shape)}/{tuple(old_v.shape)}, "
+                            f"new {tuple(new_k.shape)}/{tuple(new_v.shape)}")
+    if not (old_k.dtype == old_v.dtype == new_k.dtype == new_v.dtype):
+        raise _lib.WnwError("K and V, old and new, must share a dtype")
+    n = new_k.shape[0]
+    if cu_old.dtype != torch.int32 or cu_new.dtype != torch.int32 or cu_old.numel() != n + 1 or \
+            cu_new.numel() != n + 1:
+        raise _lib.WnwError("cu_old / cu_new must be int32 [N+1]")
+    old_k, old_v = old_k.contiguous(), old_v.contiguous()  # bound to names: must outlive the launch
+    new_k, new_v = new_k.contiguous(), new_v.contiguous()
+    cu_old, cu_new = cu_old.contiguous(), cu_new.contiguous()
+    d = old_k.shape[1]
+    out_k = torch.empty(old_k.shape[0] + n, d, dtype=old_k.dtype, device=old_k.device)
+    out_v = torch.empty_like(out_k)
+    _lib.ensure_init(old_k.device)
+    _lib.check(_lib.lib().wnw_interleave_append_kv(
+        _lib.ptr(old_k), _lib.ptr(old_v), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_old), _lib.ptr(cu_new),
+        n, old_k.shape[0], d, _lib.dtype_code(old_k.dtype), _lib.ptr(out_k), _lib.ptr(out_v),
+        _lib.stream_of(old_k.device)), "interleave_append_kv")
+    return out_k, out_v
+
 def append_inplace(
     k_pool: torch.Tensor,
     v_pool: torch.Tensor,

@@ -69,7 +69,7 @@ from torch import Tensor
 from .. import _lib
 from ..kv.flat_cache import FlatVarlenCache
 from ..kv.fused_attn import decode_attn, q1_decode_attn, q1_decode_attn_score
-from ..kv.kernels import append_inplace, interleave_append
+from ..kv.kernels import append_inplace, interleave_append_kv
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
 from .transfer import HostToDevice
@@ -745,8 +745,7 @@ class WnWCache(FlatVarlenCache):
         cu_old = self.cu_seqlens_k[layer_idx]
         new_lens = [x + 1 for x in self.seq_lens[layer_idx]]
         cu_new = cu_old + self._cu_step_increment
-        k = interleave_append(self.layer_k[layer_idx], nk, cu_old, cu_new)
-        v = interleave_append(self.layer_v[layer_idx], nv, cu_old, cu_new)
+        k, v = interleave_append_kv(self.layer_k[layer_idx], self.layer_v[layer_idx], nk, nv, cu_old, cu_new)
         self.layer_k[layer_idx], self.layer_v[layer_idx] = k, v
         self.seq_lens[layer_idx] = new_lens
         self.cu_seqlens_k[layer_idx] = cu_new
