@@ -31,6 +31,10 @@ Reported:
                     kernel on the reference's dense layout, per layer:
                     class-B segments drop their oldest window row, every
                     segment gets a new row; µs per layer and TB/s moved.
+* compaction_slack -- the same eviction as the cache's slack layout runs it
+                    (``compact_segments``: only the class-B segments move,
+                    into a free region; the append is fused into the
+                    attention launch).
 * cpu_baseline  -- the reference's decode layer-step restated in PyTorch
                     (torch.cat append + per-segment float32 attention) on the
                     host's cores, on a bounded sample of the same layers.
@@ -89,11 +93,11 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": COPY_CAL_BYTES, "launches": 3}), flush=True)
 
 
-def build_cache(cfg, dev, slack_rows: int, score: bool):
-    """A WnWCache holding the workload's state, as a prefill would leave it:
-    every layer's segments of cfg.lengths rows, no host rows, nothing
-    offloaded.  With ``score`` the class-A KV heads' query heads are
-    configured class A (scored every step)."""
+def build_cache(cfg, dev, slack_rows: int, score: bool, cls=None):
+    """A WnWCache (or ``cls``, a subclass) holding the workload's state, as a
+    prefill would leave it: every layer's segments of cfg.lengths rows, no
+    host rows, nothing offloaded.  With ``score`` the class-A KV heads' query
+    heads are configured class A (scored every step)."""
     import numpy as np
     import torch
 
@@ -107,7 +111,7 @@ def build_cache(cfg, dev, slack_rows: int, score: bool):
     conf = WnWConfig(chunk_size_s=256, overlap_s=0, token_rate=1.0, class_a=class_a, class_b=[],
                      retention_ratios=[None] * (L * Hkv), top_k_chunks=0, eviction_lag=2, prefill_score_mode="last",
                      num_layers=L, num_kv_heads=Hkv, num_q_heads=Hq)
-    cache = WnWCache(conf, L, Hkv, Hq, D, dev, slack_rows=slack_rows)
+    cache = (cls or WnWCache)(conf, L, Hkv, Hq, D, dev, slack_rows=slack_rows)
     cache.collect_stats(0)  # no memory snapshots: a captured step runs the host side once
     audio = cfg.audio.astype(np.int64)
     cache.setup_audio(torch.zeros(B, dtype=torch.int64, device=dev), torch.from_numpy(audio).to(dev), None)
@@ -304,6 +308,7 @@ def main():
         attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
 
     compact = None if args.no_compaction else compaction_timing(cfg, cache, inputs, dev)
+    compact_slack = None if args.no_compaction else slack_compaction_timing(cfg, cache, dev)
     append_t = None if args.no_compaction else append_timing(cfg, cache, inputs, dev)
     cpu = None if args.no_cpu else cpu_baseline(cfg, cache, inputs, scale, args.cpu_sample_layers)
     line = {
@@ -320,19 +325,26 @@ def main():
         "attn_only_us_per_layer_step": None if attn_us is None else round(attn_us, 3),
         "attn_only_TBs": None if attn_gbs is None else round(attn_gbs / 1e3, 4),
         "compaction": compact,
+        "compaction_slack": compact_slack,
         "append": append_t,
         "roofline": None if achieved is None else {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(cfg.name),
-            "kernel": "attn_stream_kernel, fused append + attention", "bytes_per_launch": int(fused_bytes),
-            "traffic_source": f"rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated "
-                              f"(profiles/decode_attn_{cfg.name}_traffic.json)"},
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "attn_stream_kernel, fused append + attention", "bytes_per_launch": int(fused_bytes)},
         "cpu_baseline": cpu,
     }
     rl = line["roofline"]
-    if rl is not None and rl["traffic"]:
-        # measured HBM bytes per launch over the same launch time (the
-        # counter-based rate beside the algorithmic one)
+    ratio = traffic_ratio_from_profiles(cfg.name)
+    if rl is not None and ratio is not None:
+        # the profile's measured HBM bytes per launch over its algorithmic
+        # bytes, applied to this run's launches (rows grow with the steps run,
+        # so the profiled launches and these differ in size, not in ratio)
+        rl["traffic"] = int(round(ratio * fused_bytes))
+        rl["traffic_ratio"] = round(ratio, 4)
+        rl["traffic_source"] = (f"profile-derived: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated, "
+                                f"over algorithmic bytes (profiles/decode_attn_{cfg.name}_traffic.json) x this "
+                                f"run's bytes_per_launch")
+        # the counter-based rate beside the algorithmic one
         rl["traffic_GBs"] = round(rl["traffic"] / (fused_us * 1e-6) / 1e9, 1)
     print(json.dumps(line), flush=True)
 
@@ -397,6 +409,89 @@ def compaction_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
             "workload": "dense layout, class-B segments drop row 4 (evict [4, 5)), one new row per segment"}
 
 
+def slack_move_call(cfg, cache, li: int, dev) -> tuple[dict, dict]:
+    """The slack layout's compaction of layer ``li`` as a plan runs it
+    (``wnw_compact_segments``, the cache's move of its class-B segments into
+    the free half of the flip region): every class-B segment drops row 4
+    (sink + window: the oldest window row, relative evict range [4, 5)),
+    nothing is loaded, and the segments are packed with their slack into a
+    free region (here a region of its own, sized like that half); class-A
+    segments do not move.  Returns the keyword arguments of
+    ``kernels.compact_segments`` and the move's host-side description
+    (listed segments, their new lengths and destination bases, rows moved)."""
+    import numpy as np
+    import torch
+
+    from wnw_amd.wnw.cache import _round8
+
+    D, N = cfg.head_dim, cfg.n_seg
+    i32 = dict(dtype=torch.int32, device=dev)
+    lens = np.asarray(cache.seq_lens[li], np.int64)
+    class_b = ~np.tile(cfg.class_a[li].astype(bool), cfg.batch)
+    segs = np.nonzero(class_b)[0].astype(np.int32)
+    n_ev = (class_b & (lens > 4)).astype(np.int64)
+    new_len = lens - n_ev
+    caps = np.array([_round8(int(new_len[f]) + cache.slack_rows) for f in segs], np.int64)
+    dst_base = np.zeros(N, np.int64)
+    dst_base[segs] = np.concatenate([[0], np.cumsum(caps)[:-1]]).astype(np.int64)
+    region = int(caps.sum())
+    k, v = cache.layer_k[li], cache.layer_v[li]
+    ev_off = np.concatenate([[0], np.cumsum(n_ev)]).astype(np.int32)
+    n_b = int(n_ev.sum())
+    kwargs = dict(src_k=k, src_v=v, dst_k=torch.empty(region, D, dtype=k.dtype, device=dev),
+                  dst_v=torch.empty(region, D, dtype=v.dtype, device=dev),
+                  seg_list=torch.from_numpy(segs).to(dev), src_base=cache.seg_base[li],
+                  src_len=torch.from_numpy(lens.astype(np.int32)).to(dev),
+                  dst_base=torch.from_numpy(dst_base).to(dev),
+                  new_len=torch.from_numpy(new_len.astype(np.int32)).to(dev), load_k=k[:0], load_v=v[:0],
+                  load_starts=torch.full((N,), -1, **i32), load_lens=torch.zeros(N, **i32),
+                  evict_offsets=torch.from_numpy(ev_off).to(dev), evict_starts=torch.full((n_b,), 4, **i32),
+                  evict_ends=torch.full((n_b,), 5, **i32), max_new_len=int(new_len[segs].max()) if len(segs) else 0)
+    moved = int(new_len[segs].sum())
+    return kwargs, {"segs": segs, "new_len": new_len, "dst_base": dst_base, "rows_moved": moved}
+
+
+def slack_compaction_timing(cfg, cache, dev, reps: int = 5) -> dict:
+    """The product layout's compaction (``slack_move_call``), one
+    ``compact_segments`` launch per layer, graph-replayed.  Bytes = the
+    class-B rows kept, read and written, K and V (class-A rows stay put)."""
+    import torch
+
+    from wnw_amd.wnw.kernels import compact_segments
+
+    D = cfg.head_dim
+    calls = [slack_move_call(cfg, cache, li, dev) for li in range(cfg.layers)]
+    moved = sum(info["rows_moved"] for _, info in calls) * D * 2 * 2 * 2
+    torch.cuda.synchronize()
+
+    def launches():
+        for kw, _ in calls:
+            compact_segments(**kw, check=False)
+
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        launches()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            launches()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        graph.replay()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * cfg.layers)
+    bytes_per_launch = moved / cfg.layers
+    return {"kernel": "compact_segments_kernel", "us_per_layer_step": round(us, 3),
+            "bytes_per_launch": int(bytes_per_launch),
+            "TBs": round(bytes_per_launch / (us * 1e-6) / 1e12, 3),
+            "frac_of_peak": round(bytes_per_launch / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "workload": "slack layout (the cache's plan path): every class-B segment moved into a free region "
+                        "with sink + window eviction (drop row 4), no loads; class-A segments stay"}
+
+
 def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
     """The out-of-place append of the dense layout (the reference's
     ``interleave_append`` of K and V, here one launch for both tensors,
@@ -450,17 +545,18 @@ def append_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
             "workload": "dense layout, one new row per segment, out of place (the reference operator's semantics)"}
 
 
-def traffic_from_profiles(workload: str):
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if
-    present."""
+def traffic_ratio_from_profiles(workload: str):
+    """Measured HBM bytes per launch of the dominant kernel (the committed
+    rocprofv3 PMC summary: FETCH_SIZE + WRITE_SIZE, copy-calibrated) over
+    the algorithmic bytes of the profiled launches, if present."""
     path = os.path.join(ROOT, "profiles", f"decode_attn_{workload}_traffic.json")
     if not os.path.exists(path):
         return None
     try:
         with open(path) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
-    except (OSError, ValueError):
+            d = json.load(f)
+        return d["traffic_bytes_per_launch"] / d["algorithmic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError, ZeroDivisionError):
         return None
 
 

@@ -392,7 +392,9 @@ int wnw_fused_score_accumulate(const void* q, const void* k,
  * score_offsets[b+1]); its chunks are entries chunk_offsets[b] ..
  * chunk_offsets[b+1] of chunk_starts / chunk_ends (token bounds relative to
  * the sample's first score).  A chunk's score is the mean of its scores
- * (float32 sum / max(1, length)).  out_idx [n_samples, k]
+ * (float64 prefix sums over the sample's scores, the chunk's sum divided by
+ * max(1, length) and rounded to float32; the reference takes a float32
+ * cumsum).  out_idx [n_samples, k]
  * receives each sample's k best chunks in descending order of score, equal
  * scores to the lower chunk index, -1 past the sample's chunk count.  At most
  * 8192 chunks per sample and k <= 64; bounds outside the scores set
@@ -422,7 +424,10 @@ int wnw_chunk_topk(const float* score_acc, int64_t acc_len,
  * of its pair) before gathering.  At most 64 groups.  After a HIP error the
  * job's remaining groups are not gathered, their waits return the error, and
  * the engine drains the stream.  wnw_h2d_destroy returns once every issued
- * copy has finished, so the caller may then free the staging.
+ * copy has finished, so the caller may then free the staging.  host_rows,
+ * stg_rows and dev_rows count rows of row_bytes bytes each: every array
+ * holds rows of that one size (the engine checks ranges against host_rows
+ * and the gathered rows against stg_rows and dev_rows).
  */
 typedef struct wnw_h2d wnw_h2d;
 wnw_h2d* wnw_h2d_create(int n_workers);  /* NULL on error */

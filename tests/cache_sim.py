@@ -29,15 +29,19 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 def recording(cls):
     """A cache class that records each step's score accumulator (before it is
-    cleared) and the chunk top-k handed to the planner."""
+    cleared) and the chunk top-k handed to the planner.  A step captured into
+    a HIP graph records nothing (a capture runs the host side once and may
+    not read device memory back)."""
     class Rec(cls):
         def decode_all_layers_done(self):
-            self.rec_acc.append(self.score_accumulator.double().cpu().numpy().copy())
+            if not torch.cuda.is_current_stream_capturing():
+                self.rec_acc.append(self.score_accumulator.double().cpu().numpy().copy())
             return super().decode_all_layers_done()
 
         def _plan(self, topk, off):
-            o = off.tolist()
-            self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
+            if not torch.cuda.is_current_stream_capturing():
+                o = off.tolist()
+                self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
             return super()._plan(topk, off)
     return Rec
 
@@ -47,7 +51,7 @@ def assert_topk_matches_oracle(got_per_sample, acc, offs, bounds_per_sample, k, 
     the chunk means of ``acc`` (float64 sums over each chunk's token bounds,
     oracle/planner.py).  A different choice is accepted only where the
     chunks involved are within float32 rounding of the k-th largest mean
-    (the device takes float32 prefix sums)."""
+    (the device rounds float64 prefix-sum means to float32)."""
     for b, got in enumerate(got_per_sample):
         means = op.chunk_means(acc[offs[b]:offs[b + 1]], bounds_per_sample[b])
         want = op.topk_chunks(means, k)
@@ -133,16 +137,7 @@ class DecodeSimulation:
                 self.K[l] = oracle.interleave_append(self.K[l], nk, cu_old, cu_new, dtype=oracle.DT_BF16)
                 self.V[l] = oracle.interleave_append(self.V[l], nv, cu_old, cu_new, dtype=oracle.DT_BF16)
                 self.lens[l] = [x + 1 for x in self.lens[l]]
-            dk, dv = cache.dense_kv(l)
-            np.testing.assert_array_equal(bits(dk), self.K[l], err_msg=f"K step {t} layer {l}")
-            np.testing.assert_array_equal(bits(dv), self.V[l], err_msg=f"V step {t} layer {l}")
-            cu = np.array(op.cu_from_lens(self.lens[l]), np.int32)
-            np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu, err_msg=f"cu step {t} layer {l}")
-            q_flat = bits(qs[l].reshape(B * H, G, D))
-            ref = oracle.decode_attn(q_flat, self.K[l], self.V[l], cu, self.scale, dtype=oracle.DT_BF16)
-            got = oracle.to_f64(bits(outs[l].reshape(B * H, G, D)), oracle.DT_BF16)
-            ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
-            assert ok, f"attention step {t} layer {l}: {msg}"
+            cu = self.check_layer(f"step {t}", l, qs[l], outs[l])
             qfull = bits(qs[l].reshape(B, H * G, D))
             for kv, qheads in self.groups[l]:
                 segs = [b * H + kv for b in range(B)]
@@ -151,6 +146,41 @@ class DecodeSimulation:
                                       self.scale, acc, dtype=oracle.DT_BF16)
         ok, msg = allclose_report(cache.rec_acc[t], acc, 1e-6, 1e-3)
         assert ok, f"scores step {t}: {msg}"
+
+    def check_layer(self, what: str, l: int, q=None, out=None) -> np.ndarray:
+        """The cache's layer ``l`` against the oracle's state: logical K/V rows
+        and device offsets bit-exact, host lengths equal, and with ``q`` and
+        ``out`` the attention of that step within 2e-3 + 1e-2 |ref|.
+        Returns the offsets."""
+        cache, B, H, G, D = self.cache, self.B, self.H, self.G, self.D
+        dk, dv = cache.dense_kv(l)
+        np.testing.assert_array_equal(bits(dk), self.K[l], err_msg=f"K {what} layer {l}")
+        np.testing.assert_array_equal(bits(dv), self.V[l], err_msg=f"V {what} layer {l}")
+        cu = np.array(op.cu_from_lens(self.lens[l]), np.int32)
+        np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu, err_msg=f"cu {what} layer {l}")
+        assert list(cache.seq_lens[l]) == list(self.lens[l]), f"host lengths {what} layer {l}"
+        assert cache._rows[l] == int(cu[-1]), f"host row count {what} layer {l}"
+        if out is not None:
+            q_flat = bits(q.reshape(B * H, G, D))
+            ref = oracle.decode_attn(q_flat, self.K[l], self.V[l], cu, self.scale, dtype=oracle.DT_BF16)
+            got = oracle.to_f64(bits(out.reshape(B * H, G, D)), oracle.DT_BF16)
+            ok, msg = allclose_report(got, ref, 2e-3, 1e-2)
+            assert ok, f"attention {what} layer {l}: {msg}"
+        return cu
+
+    def advance_plain(self, ks, vs) -> None:
+        """One plain decode step on the oracle's state (every segment appends
+        the step's row, no plan), checking nothing: the device work of a
+        replayed captured step."""
+        B, H, D = self.B, self.H, self.D
+        for l in range(self.L):
+            nk = bits(ks[l].reshape(B * H, D))
+            nv = bits(vs[l].reshape(B * H, D))
+            cu_old = np.array(op.cu_from_lens(self.lens[l]), np.int32)
+            cu_new = cu_old + np.arange(B * H + 1, dtype=np.int32)
+            self.K[l] = oracle.interleave_append(self.K[l], nk, cu_old, cu_new, dtype=oracle.DT_BF16)
+            self.V[l] = oracle.interleave_append(self.V[l], nv, cu_old, cu_new, dtype=oracle.DT_BF16)
+            self.lens[l] = [x + 1 for x in self.lens[l]]
 
     def final_plan(self, last_step: int) -> None:
         """The plan of the last step's scores (made by the immediate-plan cache

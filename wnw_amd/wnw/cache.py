@@ -823,13 +823,29 @@ class WnWCache(FlatVarlenCache):
         """Host bookkeeping of ``n`` decode steps that ran as replays of
         captured graphs.  A capture runs the hooks' host side once and a
         replay only the device work (the appends and the offsets they write),
-        so after replaying captured plain decode steps (no plan change, slack
-        layout, an even number of steps when two graphs alternate the offset
-        buffers) the host's lengths are advanced here."""
-        if n <= 0:
+        so after replaying captured plain decode steps the host's lengths
+        (and the native planner's) are advanced here.
+
+        Rules, each refused with ``ValueError``:
+        * slack layout, with room in every segment for the ``n`` appends;
+        * ``n`` even: a step's append reads one offsets buffer and writes the
+          other, so a replayable pair of captures alternates them, and the
+          host's current buffer is the device's again only after an even
+          number of replays;
+        * no chunk selection (``top_k_chunks`` 0): a replay skips the
+          end-of-step planning the reference runs every step, so a replayed
+          step with selection on would not be the reference's step;
+        * no plan pending (its compaction would have run in a replay)."""
+        if n == 0:
             return
+        if n < 0 or n % 2:
+            raise ValueError(f"replayed steps come in pairs of alternating captures (got {n})")
         if not self.slack_layout or n > self.decode_headroom():
             raise ValueError("replayed steps need the slack layout and room for every append")
+        if self._tk_k > 0:
+            raise ValueError("replayed steps skip the per-step chunk selection: top_k_chunks must be 0")
+        if self._pending_chunk_update:
+            raise ValueError("a plan is pending: its compaction is not part of a replayed plain step")
         for l in range(self.num_layers):
             self.seq_lens[l] = [x + n for x in self.seq_lens[l]]
             self.cu_seqlens_list[l] = None
@@ -838,6 +854,10 @@ class WnWCache(FlatVarlenCache):
             self._rows[l] += n * len(self.seq_lens[l])
         self._decode_step += n
         self._seq_lengths = [x + n for x in self._seq_lengths]
+        if self._planner is not None:
+            # the planner counts a plain step when it plans the next one; its
+            # lengths are the host's after the last plain step
+            self._planner.set_seq_lens([x for l in range(self.num_layers) for x in self.seq_lens[l]])
 
     def cu_list(self, layer_idx: int) -> list[int]:
         """Host copy of a layer's offsets (cu_seqlens_k)."""
@@ -1227,6 +1247,8 @@ class WnWCache(FlatVarlenCache):
         self.seq_lens[layer_idx] = list(new_lens)
         self.cu_seqlens_k[layer_idx] = cu_new
         self.cu_seqlens_list[layer_idx] = _build_cu_seqlens_list(new_lens)
+        self._rows[layer_idx] = self.cu_seqlens_list[layer_idx][-1]
+        self._max_len[layer_idx] = max(new_lens, default=0)
         self._pending_layers_applied += 1
         if self._pending_layers_applied == self.num_layers:
             self._pending_chunk_update = False

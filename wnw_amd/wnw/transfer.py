@@ -46,9 +46,16 @@ class HostToDevice:
         if ranges.dtype != torch.int32 or ranges.device.type != "cpu" or ranges.dim() != 2 or ranges.shape[1] != 2:
             raise _lib.WnwError("ranges must be a CPU int32 [n, 2] tensor")
         row_bytes = host_k.shape[1] * host_k.element_size()
+        # the engine counts staging and device rows in units of the host's
+        # row bytes: every array must have the host's row shape and dtype
         if host_k.shape != host_v.shape or stg_k.shape[1:] != host_k.shape[1:] or dev_k.shape[1:] != host_k.shape[1:] \
-                or dev_k.shape != dev_v.shape or stg_k.shape != stg_v.shape or dev_k.dtype != host_k.dtype:
+                or dev_k.shape != dev_v.shape or stg_k.shape != stg_v.shape or \
+                len({host_k.dtype, host_v.dtype, stg_k.dtype, stg_v.dtype, dev_k.dtype, dev_v.dtype}) != 1:
             raise _lib.WnwError("host, staging and device rows must have one row shape and dtype")
+        cur = torch.cuda.current_device()
+        if not (dev_k.is_cuda and dev_v.is_cuda and dev_k.device.index == cur and dev_v.device.index == cur
+                and dev_k.is_contiguous() and dev_v.is_contiguous()):
+            raise _lib.WnwError("device rows must be contiguous tensors on the current device")
         rg = ranges.contiguous()
         gr = (ctypes.c_int64 * len(group_ranges))(*group_ranges)
         self._keep = (rg, gr)  # the engine copies both at start; kept for symmetry with the pointers' lifetime

@@ -11,7 +11,9 @@ Choices the configuration text leaves open are fixed here and recorded in
   fraction is positive, heads drawn uniformly without replacement;
 * all seeds derive from ``seed`` (default 0) through numpy's PCG64;
 * config 5 uses sigma = 1 for the lognormal lengths;
-* config 4 selects chunks per class-B head.
+* config 4 (``wnw_amd/offload_bench.py``) selects chunks per sample, one
+  choice shared by every class-B head and layer, as the reference's planner
+  does (src/algorithms/wnw/code/cache.py:609-630).
 """
 from __future__ import annotations
 
