@@ -74,6 +74,11 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy three times (PMC byte calibration)")
+    ap.add_argument("--yardstick", action="store_true",
+                    help="only time the read-only streaming kernel (wnw_read_stream) at the attention launches' "
+                         "sizes, forms and grids")
+    ap.add_argument("--yardstick-grids", default="256,512,1024,2048")
+    ap.add_argument("--yardstick-forms", default="0,2,4,8")
     return ap.parse_args()
 
 
@@ -91,6 +96,65 @@ def copy_calibration():
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": COPY_CAL_BYTES, "launches": 3}), flush=True)
+
+
+# bytes per fused attention launch of the timed steps (the bench lines'
+# bytes_per_launch), rounded down to the yardstick's 8 KB granule
+YARDSTICK_SIZES = {"cfg2": 80265216, "cfg3": 118449152, "cfg5": 447935948}
+
+
+def yardstick(grids: list[int], forms: list[int], reps: int = 10) -> None:
+    """Read-only streaming kernel (``wnw_read_stream``) at each attention
+    launch size: a graph of launches over buffers cycled past the 256 MB
+    Infinity Cache (at least 2.4 GB in all, so every launch reads cold
+    data), replayed ``reps`` times, HIP events on the replay stream.  One
+    JSON line per (size, form, grid): µs per launch and TB/s."""
+    import torch
+
+    from wnw_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.ensure_init(dev)
+    stream = torch.cuda.Stream(device=dev)  # default priority
+    sink = torch.zeros(max(grids) * 256, dtype=torch.int32, device=dev)
+    best = {}
+    for name, size in YARDSTICK_SIZES.items():
+        size = size // 8192 * 8192
+        n_buf = max(4, -(-(2400 << 20) // size))
+        bufs = [torch.randint(-(2 ** 31), 2 ** 31 - 1, (size // 4,), dtype=torch.int32, device=dev)
+                for _ in range(n_buf)]
+        torch.cuda.synchronize()
+        for form in forms:
+            for grid in grids:
+                def launches():
+                    for b in bufs:
+                        _lib.check(_lib.lib().wnw_read_stream(_lib.ptr(b), size, grid, form, _lib.ptr(sink),
+                                                              _lib.stream_of(dev)), "read_stream")
+
+                with torch.cuda.stream(stream):
+                    launches()
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=stream):
+                        launches()
+                    g.replay()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    for _ in range(reps):
+                        g.replay()
+                    e1.record(stream)
+                    e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (reps * n_buf)
+                tbs = size / (us * 1e-6) / 1e12
+                print(json.dumps({"yardstick": name, "bytes_per_launch": size, "form": form, "grid": grid,
+                                  "us_per_launch": round(us, 3), "TBs": round(tbs, 3),
+                                  "frac_of_peak": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+                if name not in best or us < best[name]["us_per_launch"]:
+                    best[name] = {"form": form, "grid": grid, "us_per_launch": round(us, 3), "TBs": round(tbs, 3)}
+                del g
+        del bufs
+        torch.cuda.synchronize()
+    print(json.dumps({"yardstick_best": best}), flush=True)
 
 
 def build_cache(cfg, dev, slack_rows: int, score: bool, cls=None):
@@ -160,6 +224,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.yardstick:
+        yardstick([int(x) for x in args.yardstick_grids.split(",")], [int(x) for x in args.yardstick_forms.split(",")])
         return
     if args.config == "cfg4":
         from wnw_amd import offload_bench

@@ -540,6 +540,24 @@ int wnw_gather_host_rows(const void* host_k, const void* host_v,
                          int64_t row_bytes, void* out_k, void* out_v,
                          int64_t out_rows, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Measurement                                                               */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Read-only streaming yardstick: reads `bytes` (a multiple of 8192) from the
+ * device buffer `src` with n_wg workgroups of 256 threads, workgroup i
+ * reading the i-th contiguous share.  form 2, 4 or 8: per thread two
+ * batches of that many 16-byte loads in flight into registers; form 0: the
+ * decode attention kernel's load path (1 KB direct-to-LDS loads, two 8 KB
+ * steps in flight per wave).  sink (n_wg * 256 uint32) is written only when
+ * a workgroup's XOR of what it read equals a fixed constant.  No
+ * counterpart in the reference: it measures what a single launch of a given
+ * size reaches when it only reads, beside the attention launch.
+ */
+int wnw_read_stream(const void* src, int64_t bytes, int64_t n_wg, int form,
+                    void* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,30 +31,46 @@ __global__ __launch_bounds__(256) void read_stream_vgpr_kernel(const u32x4* __re
   constexpr int64_t kBatch = (int64_t)U * 256;
   int64_t i = lo + threadIdx.x;
   u32x4 a[U], b[U];
+  // every load is issued (index clamped to the share's last chunk, which
+  // exists: hi >= 1), and the chunks past the share are dropped after
+  // arrival, so no load waits behind a branch
+  const int64_t last = hi - 1;
   auto load = [&](u32x4 (&r)[U], int64_t at) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = at + (int64_t)u * 256;
-      r[u] = j < hi ? s[j] : u32x4{0, 0, 0, 0};
+      r[u] = s[j < hi ? j : last];
     }
+    __builtin_amdgcn_sched_barrier(0);  // the whole batch is issued before anything is consumed
   };
-  auto eat = [&](const u32x4 (&r)[U]) {
+  auto eat = [&](const u32x4 (&r)[U], int64_t at) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc ^= r[u];
-  };
-  load(a, i);
-  i += kBatch;
-  while (i - kBatch < hi) {
-    load(b, i);
-    i += kBatch;
-    eat(a);
-    if (i - kBatch >= hi) {
-      eat(b);
-      break;
+    for (int u = 0; u < U; ++u) {
+      const bool in = at + (int64_t)u * 256 < hi;
+      acc ^= in ? r[u] : u32x4{0, 0, 0, 0};
     }
+  };
+  // batches at i (a) and i + kBatch (b) in flight; the loop eats a, loads
+  // the batch after b into a, then eats b
+  if (i < hi) {
     load(a, i);
-    i += kBatch;
-    eat(b);
+    while (true) {
+      const int64_t ib = i + kBatch;
+      if (ib >= hi) {
+        eat(a, i);
+        break;
+      }
+      load(b, ib);
+      eat(a, i);
+      const int64_t ia = ib + kBatch;
+      if (ia >= hi) {
+        eat(b, ib);
+        break;
+      }
+      load(a, ia);
+      eat(b, ib);
+      i = ia;
+    }
   }
   const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
   if (x == 0x9e3779b9u) sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = x;
@@ -95,8 +111,6 @@ __global__ __launch_bounds__(256) void read_stream_lds_kernel(const uint8_t* __r
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(
       const __attribute__((address_space(3))) void*)&ring[w][0][0]);
   auto issue = [&](int64_t step, int b) {
-    const uint8_t* g = (const uint8_t*)__builtin_amdgcn_readfirstlane((uint32_t)0) + 0;
-    (void)g;
     const void* base = src + step * SB;
 #pragma unroll
     for (int u = 0; u < NI; ++u) ys_dma16(base, (uint32_t)(u * 1024 + lane * 16), lds0 + b * SB + u * 1024);
