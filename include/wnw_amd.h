@@ -437,6 +437,25 @@ int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v,
                   const int64_t* group_ranges, int n_groups, void* stg_k,
                   void* stg_v, int64_t stg_rows, void* dev_k, void* dev_v,
                   int64_t dev_rows, int64_t row_bytes, void* stream);
+/*
+ * wnw_h2d_start without the host gather: stage_k / stage_v are DEVICE rows
+ * (stage_rows of row_bytes, at least the job's rows).  Per group, the
+ * ranges are taken in host-row order and merged where they touch in host
+ * memory; each merged span is copied by the DMA engines straight from
+ * host_k / host_v into the group's stage rows, and a kernel on `stream` then
+ * moves every range to its transfer-order rows of dev_k / dev_v before the
+ * group's event (the same rows wnw_h2d_start fills).  Host rows laid out so
+ * that a segment's rows of consecutive layers are adjacent make a group a
+ * few large copies.  row_bytes a multiple of 16; stage and device rows
+ * 16-byte aligned.  wait / join / destroy as for wnw_h2d_start; the two
+ * forms may alternate on one engine.
+ */
+int wnw_h2d_start_direct(wnw_h2d* x, const void* host_k, const void* host_v,
+                         int64_t host_rows, const int32_t* ranges,
+                         int64_t n_ranges, const int64_t* group_ranges,
+                         int n_groups, void* stage_k, void* stage_v,
+                         int64_t stage_rows, void* dev_k, void* dev_v,
+                         int64_t dev_rows, int64_t row_bytes, void* stream);
 int wnw_h2d_wait(wnw_h2d* x, int group, void* stream);
 int wnw_h2d_join(wnw_h2d* x);
 

@@ -64,11 +64,13 @@ LAYOUTS = {"slack": dict(slack_rows=256), "tight": dict(slack_rows=3, tail=0), "
 @pytest.mark.parametrize("layout", ["slack", "tight", "dense"])
 @pytest.mark.parametrize("variant,fused,offload", [("wnw", True, "copy"), ("wnw", False, "copy"),
                                                    ("wnw_fallback", True, "copy"), ("wnw_cpp", True, "copy"),
+                                                   ("wnw", True, "staged"), ("wnw_cpp", True, "staged"),
                                                    ("wnw", True, "device"), ("wnw_cpp", True, "device")])
 def test_decode_steps_match_simulation(variant, fused, offload, layout, monkeypatch):
     dev = torch.device("cuda", 0)
-    # loads through the transfer engine (host gather threads + DMA copies) or
-    # the device gather kernel reading pinned memory
+    # loads through the transfer engine (DMA copies straight from the host
+    # rows into a device stage, or host gather threads into pinned staging
+    # + DMA copies) or the device gather kernel reading pinned memory
     monkeypatch.setenv("WNW_OFFLOAD", offload)
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)

@@ -51,11 +51,12 @@ def _config():
                      prefill_score_mode="last", num_layers=L, num_kv_heads=HKV, num_q_heads=HQ)
 
 
-@pytest.mark.parametrize("fused,offload", [(True, "copy"), (False, "copy"), (True, "device")])
+@pytest.mark.parametrize("fused,offload", [(True, "copy"), (False, "copy"), (True, "staged"), (True, "device")])
 def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
     dev = torch.device("cuda", 0)
-    # the transfer engine (host gather threads + DMA copies per group of
-    # layers) or the device gather kernel reading pinned memory
+    # the transfer engine (DMA copies straight from the host rows, or host
+    # gather threads + DMA copies, per group of layers) or the device gather
+    # kernel reading pinned memory
     monkeypatch.setenv("WNW_OFFLOAD", offload)
     cfg = _config()
     cache = recording(WnWCache)(cfg, L, HKV, HQ, D, dev)

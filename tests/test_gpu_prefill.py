@@ -4,7 +4,8 @@ Random bf16 K/V of two layers and three left-padded samples go through
 ``setup_audio`` (with an attention mask), ``prefill_after_attn`` per layer
 and ``prefill_all_layers_done``.  The flat layers, their offsets, the
 pinned host rows, ``restore_meta``, the loaded segments and the native
-planner's view of them must equal ``oracle.prefill``'s.  Per-head scores
+planner's view of them must equal ``oracle.prefill``'s (the host rows
+through ``restore_meta``: the cache keeps them in another order).  Per-head scores
 are distinct values and the class-A sums give well separated chunk means,
 so no selection depends on a tie order.
 """
@@ -77,15 +78,28 @@ def test_prefill_matches_restatement(gpu, global_topk):
         assert list(cache.seq_lens[l]) == list(pf.seq_lens[l])
         cu = np.concatenate([[0], np.cumsum(pf.seq_lens[l])]).astype(np.int32)
         np.testing.assert_array_equal(cache.cu_seqlens_k[l].cpu().numpy(), cu)
+    # the host rows: the same rows per (layer, sample, head, segment) through
+    # restore_meta (bit-exact), the same residency offsets; the cache keeps
+    # them in (sample, segment, layer, head) order, the restatement in the
+    # reference's (layer, sample, head, segment) order
+    hk, hv = _bits(cache.cpu_restore_k), _bits(cache.cpu_restore_v)
+    assert hk.shape == pf.cpu_k.shape and hv.shape == pf.cpu_v.shape
+    placed = []
+    for l in range(L):
         for b in range(B):
             for h in range(H):
-                got = [None if m is None else (m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
-                       for m in cache.restore_meta[l][b][h]]
-                want = [None if m is None else (m.cpu_start, m.cpu_end, m.gpu_rel_start, m.gpu_rel_end)
-                        for m in pf.meta[l][b][h]]
-                assert got == want, f"restore_meta layer {l} sample {b} head {h}"
-    np.testing.assert_array_equal(_bits(cache.cpu_restore_k), pf.cpu_k)
-    np.testing.assert_array_equal(_bits(cache.cpu_restore_v), pf.cpu_v)
+                for si, (m, w) in enumerate(zip(cache.restore_meta[l][b][h], pf.meta[l][b][h])):
+                    assert (m is None) == (w is None), f"restore_meta layer {l} sample {b} head {h} seg {si}"
+                    if m is None:
+                        continue
+                    assert (m.gpu_rel_start, m.gpu_rel_end) == (w.gpu_rel_start, w.gpu_rel_end)
+                    assert m.cpu_end - m.cpu_start == w.cpu_end - w.cpu_start
+                    np.testing.assert_array_equal(hk[m.cpu_start:m.cpu_end], pf.cpu_k[w.cpu_start:w.cpu_end])
+                    np.testing.assert_array_equal(hv[m.cpu_start:m.cpu_end], pf.cpu_v[w.cpu_start:w.cpu_end])
+                    placed.append(((b, si, l, h), m.cpu_start, m.cpu_end))
+    placed.sort()
+    assert [p[1] for p in placed] == [0] + [p[2] for p in placed[:-1]] and placed[-1][2] == hk.shape[0], \
+        "host rows in (sample, segment, layer, head) order, back to back"
     assert cache.cpu_restore_k.is_pinned()
     for b in range(B):
         assert set(cache.loaded_segments[b]) == pf.loaded[b]

@@ -70,6 +70,79 @@ def test_ranges_land_in_transfer_order_over_several_starts():
     eng.close()
 
 
+def _chunky_case(rng, host_rows, n_groups):
+    """Ranges as a plan over a (sample, segment, layer, head) host layout
+    makes them: runs of ranges that touch in host memory (one run per
+    segment and group), listed in another order (transfer order), with some
+    empty, repeated and overlapping ranges."""
+    runs, at = [], 0
+    while at < host_rows - 2000:
+        n = int(rng.integers(1, 12))
+        lens = rng.integers(0, 150, n)
+        run = []
+        for x in lens:
+            run.append((at, at + int(x)))
+            at += int(x)
+        runs.append(run)
+        at += int(rng.integers(0, 500))
+    picks = [runs[i] for i in rng.choice(len(runs), size=min(len(runs), 24), replace=False)]
+    ranges = [r for run in picks for r in run]
+    ranges += [ranges[int(i)] for i in rng.integers(0, len(ranges), 5)]  # repeats
+    s0 = int(rng.integers(0, host_rows - 400))
+    ranges += [(s0, s0 + 300), (s0 + 100, s0 + 200)]  # overlapping
+    order = rng.permutation(len(ranges))
+    ranges = np.array([ranges[i] for i in order], dtype=np.int32)
+    cuts = np.sort(rng.integers(0, len(ranges) + 1, n_groups - 1))
+    return ranges, [0] + cuts.tolist() + [len(ranges)]
+
+
+def test_direct_form_lands_in_transfer_order():
+    """wnw_h2d_start_direct (DMA of merged spans into a device stage, then a
+    permute kernel) fills the same rows as the staged form, over several
+    starts that alternate the two forms on one engine."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(15)
+    hk_np, hk = _host_rows(rng, 30000)
+    hv_np, hv = _host_rows(rng, 30000)
+    eng = HostToDevice(workers=4)
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        stage = (torch.empty(40000, D, dtype=torch.bfloat16, device=dev),
+                 torch.empty(40000, D, dtype=torch.bfloat16, device=dev))
+    stg = [(torch.empty(40000, D, dtype=torch.bfloat16, pin_memory=True),
+            torch.empty(40000, D, dtype=torch.bfloat16, pin_memory=True)) for _ in range(2)]
+    outs = []
+    for job in range(6):
+        ranges, bounds = _chunky_case(rng, 30000, int(rng.integers(1, 9)))
+        total = int((ranges[:, 1] - ranges[:, 0]).sum())
+        assert total <= 40000
+        with torch.cuda.stream(stream):
+            dk = torch.empty(max(total, 1), D, dtype=torch.bfloat16, device=dev)
+            dv = torch.empty_like(dk)
+        direct = job % 3 != 2
+        print(f"job {job}: {'direct' if direct else 'staged'}, {len(ranges)} ranges, {len(bounds) - 1} groups, "
+              f"{total} rows", flush=True)
+        if direct:
+            eng.start_direct(hk, hv, torch.from_numpy(ranges), bounds, stage[0], stage[1], dk, dv, stream)
+        else:
+            eng.start(hk, hv, torch.from_numpy(ranges), bounds, *stg[job % 2], dk, dv, stream)
+        compute = torch.cuda.current_stream(dev)
+        for g in range(len(bounds) - 1):
+            eng.wait(g, compute)
+        outs.append((ranges, dk[:total].clone(), dv[:total].clone()))
+    eng.join()
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    for ranges, got_k, got_v in outs:
+        idx = np.concatenate([np.arange(s, e) for s, e in ranges])
+        np.testing.assert_array_equal(got_k.cpu().view(torch.int16).numpy().view(np.uint16), hk_np[idx])
+        np.testing.assert_array_equal(got_v.cpu().view(torch.int16).numpy().view(np.uint16), hv_np[idx])
+    with pytest.raises(_lib.WnwError):  # more rows than the stage holds
+        eng.start_direct(hk, hv, torch.tensor([[0, 20000]], dtype=torch.int32), [0, 1], stage[0][:100],
+                         stage[1][:100], dk, dv, stream)
+    eng.close()
+
+
 def test_arguments_are_checked():
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(6)

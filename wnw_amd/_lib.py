@@ -77,6 +77,8 @@ _SIGNATURES = {
     "wnw_h2d_create": (_vp, [_i32]),
     "wnw_h2d_destroy": (None, [_vp]),
     "wnw_h2d_start": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp]),
+    "wnw_h2d_start_direct": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _i64,
+                                    _vp]),
     "wnw_h2d_wait": (_i32, [_vp, _i32, _vp]),
     "wnw_h2d_join": (_i32, [_vp]),
 }

@@ -9,8 +9,9 @@
 // runs on one thread and one copy carries every layer's rows, so the first
 // layer's rebuild waits for the whole transfer.
 //
-// Here the ranges (in transfer order: layer, sample, head, segment) are
-// split into groups of consecutive layers.  A background thread per
+// Two forms of a job.  Staged (wnw_h2d_start): the ranges (in transfer
+// order: layer, sample, head, segment) are split into groups of consecutive
+// layers.  A background thread per
 // engine walks the groups: a pool of worker threads memcpys the group's
 // ranges into the staging rows (ranges split evenly over the workers,
 // written with streaming stores: the staging is read by the DMA engines
@@ -21,6 +22,17 @@
 // gathers and copies overlap earlier layers' compute, and the copies run on
 // the DMA engines: unlike a kernel reading pinned host memory, they leave
 // the compute kernels' memory traffic alone.
+//
+// Direct (wnw_h2d_start_direct): no host gather at all.  A group's ranges
+// are taken in host-row order, ranges that touch in host memory are merged
+// into spans, and each span is copied by the DMA engines straight from the
+// pinned host rows into the group's rows of a device stage buffer (in that
+// host order); a kernel on the same stream then moves every range from the
+// stage to its transfer-order rows of the outputs, and the group's event is
+// recorded.  With a host layout that keeps a segment's rows of consecutive
+// layers together, a group is a few large spans, so the host link is the
+// only bound (the staged form's host memcpy reads and writes every row once
+// more in host memory, which is what kept the DMA engines waiting).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,7 +64,50 @@ struct Job {
   hipStream_t stream = nullptr;
   int device = 0;
   int parity = 0;
+  // direct form: stg_k / stg_v are the device stage rows, and stage_of[r]
+  // is range r's first stage row (the group's ranges in host order)
+  bool direct = false;
+  std::vector<int64_t> stage_of;
+  int64_t stage_rows = 0, dev_rows = 0;
 };
+
+// Direct form: per range (stage row, output row, rows), int64, read by
+// stage_permute_kernel.
+constexpr int kDescWords = 3;
+
+// Rows of the device stage moved to their transfer-order rows: ranges
+// r = blockIdx.x, blockIdx.x + gridDim.x, ..., tensor blockIdx.y (0: K,
+// 1: V).  A range outside either array raises WNW_DEVERR_BOUNDS and is
+// skipped.
+__global__ __launch_bounds__(256) void stage_permute_kernel(const wnw::u32x4* stage_k, const wnw::u32x4* stage_v,
+                                                            int64_t stage_rows, const int64_t* desc, int64_t n,
+                                                            int64_t row_vec, wnw::u32x4* out_k, wnw::u32x4* out_v,
+                                                            int64_t out_rows, int32_t* err) {
+  using wnw::u32x4;
+  const u32x4* src = blockIdx.y ? stage_v : stage_k;
+  u32x4* dst = blockIdx.y ? out_v : out_k;
+  const WNW_GLOBAL int64_t* dsc = wnw::gptr<int64_t>(desc);
+  for (int64_t r = blockIdx.x; r < n; r += gridDim.x) {
+    const int64_t s = dsc[kDescWords * r], d = dsc[kDescWords * r + 1], len = dsc[kDescWords * r + 2];
+    if (s < 0 || d < 0 || len < 0 || s + len > stage_rows || d + len > out_rows) {
+      if (threadIdx.x == 0) wnw::raise_device_error(err, WNW_DEVERR_BOUNDS);
+      continue;
+    }
+    const u32x4* sp = src + s * row_vec;
+    WNW_GLOBAL u32x4* dp = wnw::gptr_w<u32x4>(dst + d * row_vec);
+    const int64_t nv = len * row_vec;
+    constexpr int U = 4;  // 16-byte loads in flight per thread
+    int64_t i = threadIdx.x;
+    for (; i + (U - 1) * 256 < nv; i += U * 256) {
+      u32x4 a[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(sp + i + u * 256);
+#pragma unroll
+      for (int u = 0; u < U; ++u) dp[i + u * 256] = a[u];
+    }
+    for (; i < nv; i += 256) dp[i] = __builtin_nontemporal_load(sp + i);
+  }
+}
 
 }  // namespace
 
@@ -79,6 +134,20 @@ struct wnw_h2d {
   int last_groups[2] = {0, 0};
   int parity = 0;
   int n_workers = 0;
+  // direct form, per parity: a job's permute descriptors (pinned host copy
+  // and device copy), grown by the lead thread once the parity's previous
+  // job is done with them
+  int64_t* desc_host[2] = {nullptr, nullptr};
+  int64_t* desc_dev[2] = {nullptr, nullptr};
+  int64_t desc_cap[2] = {0, 0};  // ranges each pair holds
+  // direct form: the V spans go on a second stream (a second DMA engine),
+  // which hides the fixed cost of each copy behind the other stream's
+  // transfers; per parity the job-start event it waits for and per group
+  // the end of its V copies, which the job's stream waits for
+  hipStream_t aux = nullptr;
+  int aux_device = -1;
+  hipEvent_t ev_start[2] = {};
+  hipEvent_t ev_v[2][kMaxGroups] = {};
 };
 
 namespace {
@@ -116,6 +185,98 @@ void worker_loop(wnw_h2d* x, int w) {
   }
 }
 
+// Records the first HIP error of the current job (its text is re-raised by
+// wait / join) and marks group g issued.
+void note_issued(wnw_h2d* x, hipError_t e, int g) {
+  std::lock_guard<std::mutex> lk(x->mu);
+  if (e != hipSuccess && x->error == WNW_OK) {
+    snprintf(x->error_msg, sizeof(x->error_msg), "h2d: %s (%d)", hipGetErrorString(e), (int)e);
+    x->error = WNW_EHIP;
+  }
+  x->issued = g;
+  x->cv_issued.notify_all();
+}
+
+// The direct form of a job (lead thread, after the wait for the parity's
+// previous job): per group the spans' DMA copies into the stage, the
+// group's permute descriptors (one small copy), the permute kernel and the
+// group's event.  Returns the number of groups whose event is recorded.
+int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
+  const int p = j.parity;
+  const int64_t n = (int64_t)j.ranges.size() / 2;
+  if (e == hipSuccess && n > x->desc_cap[p]) {  // the parity's previous job is done with these
+    if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
+    if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
+    x->desc_host[p] = nullptr;
+    x->desc_dev[p] = nullptr;
+    x->desc_cap[p] = 0;
+    const int64_t cap = std::max<int64_t>(n, 1024);
+    e = hipHostMalloc((void**)&x->desc_host[p], (size_t)cap * kDescWords * 8, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc((void**)&x->desc_dev[p], (size_t)cap * kDescWords * 8);
+    if (e == hipSuccess) x->desc_cap[p] = cap;
+  }
+  if (e == hipSuccess && (x->aux == nullptr || x->aux_device != j.device)) {
+    if (x->aux) (void)hipStreamDestroy(x->aux);
+    x->aux = nullptr;
+    e = hipStreamCreateWithFlags(&x->aux, hipStreamNonBlocking);  // default priority
+    if (e == hipSuccess) x->aux_device = j.device;
+  }
+  // the aux stream's copies follow everything queued on the job's stream
+  // before this job (the previous job's permutes read the stage rows)
+  if (e == hipSuccess) e = hipEventRecord(x->ev_start[p], j.stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux, x->ev_start[p], 0);
+  int recorded = 0;
+  const int64_t rb = j.row_bytes;
+  std::vector<int64_t> ord;
+  for (int g = 0; g < x->groups; ++g) {
+    const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
+    if (e == hipSuccess && b > a) {
+      // the group's ranges in host order (their stage order), merged into
+      // spans where they touch in host memory
+      ord.resize(b - a);
+      for (int64_t r = a; r < b; ++r) ord[r - a] = r;
+      std::sort(ord.begin(), ord.end(), [&](int64_t u, int64_t v) { return j.stage_of[u] < j.stage_of[v]; });
+      for (size_t i = 0; i < ord.size() && e == hipSuccess;) {
+        const int64_t r0 = ord[i];
+        const int64_t h0 = j.ranges[2 * r0], st0 = j.stage_of[r0];
+        int64_t h1 = j.ranges[2 * r0 + 1];
+        size_t k = i + 1;
+        while (k < ord.size() && j.ranges[2 * ord[k]] == h1) h1 = j.ranges[2 * ord[k++] + 1];
+        if (h1 > h0) {
+          const size_t bytes = (size_t)((h1 - h0) * rb);
+          e = hipMemcpyAsync(j.stg_k + st0 * rb, j.host_k + h0 * rb, bytes, hipMemcpyHostToDevice, j.stream);
+          if (e == hipSuccess)
+            e = hipMemcpyAsync(j.stg_v + st0 * rb, j.host_v + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux);
+        }
+        i = k;
+      }
+      if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux);
+      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_v[p][g], 0);
+      int64_t* dh = x->desc_host[p] + a * kDescWords;
+      for (int64_t r = a; r < b; ++r) {
+        dh[(r - a) * kDescWords] = j.stage_of[r];
+        dh[(r - a) * kDescWords + 1] = j.dst[r];
+        dh[(r - a) * kDescWords + 2] = (int64_t)j.ranges[2 * r + 1] - j.ranges[2 * r];
+      }
+      int64_t* dd = x->desc_dev[p] + a * kDescWords;
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(dd, dh, (size_t)(b - a) * kDescWords * 8, hipMemcpyHostToDevice, j.stream);
+      if (e == hipSuccess) {
+        const unsigned grid = (unsigned)std::min<int64_t>(b - a, 1024);
+        hipLaunchKernelGGL(stage_permute_kernel, dim3(grid, 2), dim3(256), 0, j.stream,
+                           (const wnw::u32x4*)j.stg_k, (const wnw::u32x4*)j.stg_v, j.stage_rows, dd, b - a,
+                           rb / 16, (wnw::u32x4*)j.dev_k, (wnw::u32x4*)j.dev_v, j.dev_rows,
+                           wnw::device_error_word());
+        e = hipGetLastError();
+      }
+    }
+    if (e == hipSuccess) e = hipEventRecord(x->events[p][g], j.stream);
+    if (e == hipSuccess) recorded = g + 1;
+    note_issued(x, e, g);
+  }
+  return recorded;
+}
+
 void lead_loop(wnw_h2d* x) {
   for (;;) {
     {
@@ -133,7 +294,8 @@ void lead_loop(wnw_h2d* x) {
     if (e == hipSuccess && x->last_groups[j.parity] > 0)
       e = hipEventSynchronize(x->events[j.parity][x->last_groups[j.parity] - 1]);
     int recorded = 0;
-    for (int g = 0; g < x->groups; ++g) {
+    if (j.direct) recorded = run_direct(x, j, e);
+    for (int g = 0; g < x->groups && !j.direct; ++g) {
       if (e == hipSuccess) {  // after an error the staging is left alone (copies may still read it)
         std::unique_lock<std::mutex> lk(x->mu);
         x->task_group = g;
@@ -166,6 +328,7 @@ void lead_loop(wnw_h2d* x) {
     // so the next job of this parity has nothing to wait for
     if (recorded < x->groups) {
       (void)hipStreamSynchronize(j.stream);
+      if (x->aux) (void)hipStreamSynchronize(x->aux);
       recorded = 0;
     }
     {
@@ -201,6 +364,24 @@ extern "C" wnw_h2d* wnw_h2d_create(int n_workers) {
         return nullptr;
       }
     }
+  bool ok = true;
+  for (int p = 0; p < 2; ++p) {
+    ok = ok && hipEventCreateWithFlags(&x->ev_start[p], hipEventDisableTiming) == hipSuccess;
+    for (int g = 0; g < kMaxGroups; ++g)
+      ok = ok && hipEventCreateWithFlags(&x->ev_v[p][g], hipEventDisableTiming) == hipSuccess;
+  }
+  if (!ok) {
+    wnw::set_error("h2d: event creation failed");
+    for (int p = 0; p < 2; ++p) {
+      if (x->ev_start[p]) (void)hipEventDestroy(x->ev_start[p]);
+      for (int g = 0; g < kMaxGroups; ++g) {
+        if (x->events[p][g]) (void)hipEventDestroy(x->events[p][g]);
+        if (x->ev_v[p][g]) (void)hipEventDestroy(x->ev_v[p][g]);
+      }
+    }
+    delete x;
+    return nullptr;
+  }
   x->n_workers = n_workers;
   for (int w = 0; w < n_workers; ++w) x->workers.emplace_back(worker_loop, x, w);
   x->lead = std::thread(lead_loop, x);
@@ -224,14 +405,24 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
     if (x->last_groups[p] > 0) (void)hipEventSynchronize(x->events[p][x->last_groups[p] - 1]);
   for (int p = 0; p < 2; ++p)
     for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->events[p][g]);
+  if (x->aux) (void)hipStreamSynchronize(x->aux);
+  for (int p = 0; p < 2; ++p) {
+    if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
+    if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
+    (void)hipEventDestroy(x->ev_start[p]);
+    for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->ev_v[p][g]);
+  }
+  if (x->aux) (void)hipStreamDestroy(x->aux);
   delete x;
 }
 
-extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v, int64_t host_rows,
-                             const int32_t* ranges, int64_t n_ranges, const int64_t* group_ranges, int n_groups,
-                             void* stg_k, void* stg_v, int64_t stg_rows, void* dev_k, void* dev_v, int64_t dev_rows,
-                             int64_t row_bytes, void* stream) {
-  WNW_CHECK_ARG(x, "h2d: null engine");
+namespace {
+
+// Checks the arguments of a start and fills the job's ranges, rows and
+// pointers (both forms).
+int make_job(Job& j, const void* host_k, const void* host_v, int64_t host_rows, const int32_t* ranges,
+             int64_t n_ranges, const int64_t* group_ranges, int n_groups, void* stg_k, void* stg_v, int64_t stg_rows,
+             void* dev_k, void* dev_v, int64_t dev_rows, int64_t row_bytes, void* stream) {
   WNW_CHECK_ARG(n_groups >= 1 && n_groups <= kMaxGroups, "h2d: n_groups must be in [1, %d]", kMaxGroups);
   WNW_CHECK_ARG(n_ranges >= 0 && row_bytes > 0, "h2d: bad sizes");
   WNW_CHECK_ARG(group_ranges && group_ranges[0] == 0 && group_ranges[n_groups] == n_ranges,
@@ -240,7 +431,6 @@ extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v,
     WNW_CHECK_ARG(group_ranges[g] <= group_ranges[g + 1], "h2d: group bounds decrease");
   WNW_CHECK_ARG(n_ranges == 0 || (ranges && host_k && host_v && stg_k && stg_v && dev_k && dev_v),
                 "h2d: null pointer argument");
-  Job j;
   j.ranges.assign(ranges, ranges + 2 * n_ranges);
   j.dst.resize(n_ranges + 1);
   j.dst[0] = 0;
@@ -261,8 +451,15 @@ extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v,
   j.dev_k = (char*)dev_k;
   j.dev_v = (char*)dev_v;
   j.row_bytes = row_bytes;
+  j.stage_rows = stg_rows;
+  j.dev_rows = dev_rows;
   j.stream = (hipStream_t)stream;
   WNW_CHECK_HIP(hipGetDevice(&j.device), "h2d: hipGetDevice");
+  return WNW_OK;
+}
+
+// Hands a job to the lead thread (after the previous job is fully issued).
+void submit(wnw_h2d* x, Job&& j, int n_groups) {
   {
     std::unique_lock<std::mutex> lk(x->mu);
     join_locked(x, lk);  // the previous job's groups are issued; its events stay valid (other parity)
@@ -276,6 +473,53 @@ extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v,
     x->job_pending = true;
   }
   x->cv_job.notify_all();
+}
+
+}  // namespace
+
+extern "C" int wnw_h2d_start(wnw_h2d* x, const void* host_k, const void* host_v, int64_t host_rows,
+                             const int32_t* ranges, int64_t n_ranges, const int64_t* group_ranges, int n_groups,
+                             void* stg_k, void* stg_v, int64_t stg_rows, void* dev_k, void* dev_v, int64_t dev_rows,
+                             int64_t row_bytes, void* stream) {
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  Job j;
+  const int rc = make_job(j, host_k, host_v, host_rows, ranges, n_ranges, group_ranges, n_groups, stg_k, stg_v,
+                          stg_rows, dev_k, dev_v, dev_rows, row_bytes, stream);
+  if (rc != WNW_OK) return rc;
+  submit(x, std::move(j), n_groups);
+  return WNW_OK;
+}
+
+extern "C" int wnw_h2d_start_direct(wnw_h2d* x, const void* host_k, const void* host_v, int64_t host_rows,
+                                    const int32_t* ranges, int64_t n_ranges, const int64_t* group_ranges,
+                                    int n_groups, void* stage_k, void* stage_v, int64_t stage_rows, void* dev_k,
+                                    void* dev_v, int64_t dev_rows, int64_t row_bytes, void* stream) {
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  WNW_CHECK_ARG(row_bytes % 16 == 0, "h2d: row_bytes must be a multiple of 16");
+  Job j;
+  const int rc = make_job(j, host_k, host_v, host_rows, ranges, n_ranges, group_ranges, n_groups, stage_k,
+                          stage_v, stage_rows, dev_k, dev_v, dev_rows, row_bytes, stream);
+  if (rc != WNW_OK) return rc;
+  WNW_CHECK_ARG(n_ranges == 0 || (((uintptr_t)stage_k | (uintptr_t)stage_v | (uintptr_t)dev_k | (uintptr_t)dev_v) &
+                                  15) == 0,
+                "h2d: stage and device rows must be 16-byte aligned");
+  // stage rows: each group's rows [dst[a], dst[b]) hold its ranges in host order
+  j.direct = true;
+  j.stage_of.assign(n_ranges, 0);
+  std::vector<int64_t> ord;
+  for (int g = 0; g < n_groups; ++g) {
+    const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
+    ord.resize(b - a);
+    for (int64_t r = a; r < b; ++r) ord[r - a] = r;
+    std::stable_sort(ord.begin(), ord.end(),
+                     [&](int64_t u, int64_t v) { return j.ranges[2 * u] < j.ranges[2 * v]; });
+    int64_t at = j.dst[a];
+    for (int64_t r : ord) {
+      j.stage_of[r] = at;
+      at += (int64_t)j.ranges[2 * r + 1] - j.ranges[2 * r];
+    }
+  }
+  submit(x, std::move(j), n_groups);
   return WNW_OK;
 }
 

@@ -63,6 +63,7 @@ import os
 from dataclasses import dataclass
 from itertools import accumulate
 
+import numpy as np
 import torch
 from torch import Tensor
 
@@ -375,10 +376,17 @@ class WnWCache(FlatVarlenCache):
         """cache.py:339-390: pin the host rows, index them, load the initial
         top-k chunks, hand the state to the native planner."""
         if self._cpu_buffers_k:
-            self.cpu_restore_k = torch.cat(self._cpu_buffers_k).pin_memory()
-            self.cpu_restore_v = torch.cat(self._cpu_buffers_v).pin_memory()
+            # host order (sample, segment, layer, head): a segment's rows of
+            # consecutive layers are adjacent, so a plan's loads of a group of
+            # layers are one span per (sample, segment) for the DMA engines;
+            # restore_meta indexes the rows as in the reference
+            metas = self._cpu_buffer_metas
+            order = sorted(range(len(metas)), key=lambda i: (metas[i][1], metas[i][3], metas[i][0], metas[i][2]))
+            self.cpu_restore_k = torch.cat([self._cpu_buffers_k[i] for i in order]).pin_memory()
+            self.cpu_restore_v = torch.cat([self._cpu_buffers_v[i] for i in order]).pin_memory()
             o = 0
-            for l, b, h, si, n in self._cpu_buffer_metas:
+            for i in order:
+                l, b, h, si, n = metas[i]
                 self.restore_meta[l][b][h][si] = SegmentMeta(o, o + n)
                 o += n
         else:
@@ -629,28 +637,36 @@ class WnWCache(FlatVarlenCache):
         # gather waits only for the copy that used its pair two plans ago
         self._staging = [None, None]
         self._staging_turn = 0
-        # the offload channel (WNW_OFFLOAD): "copy" (default), the transfer
-        # engine -- host gather threads and DMA copies per group of layers
-        # on a side stream, which leave the compute kernels' memory traffic
-        # alone; "device", a gather kernel reading the pinned restore rows
-        # itself (its reads of host memory outrun the copy engine, but the
-        # compute kernels that run meanwhile slow down by more than that)
+        # the offload channel (WNW_OFFLOAD), per group of layers on a side
+        # stream, a layer waiting for its own group only:
+        # "copy" (default), the transfer engine's direct form -- the DMA
+        #   engines copy the plan's rows straight from the pinned restore
+        #   rows (merged spans) into a device stage, a kernel puts them in
+        #   transfer order; the host copies nothing;
+        # "staged", the transfer engine's staged form -- host threads gather
+        #   the rows into pinned staging, the DMA engines copy that;
+        # "device", a gather kernel reading the pinned restore rows itself
+        #   (its reads of host memory outrun the copy engine, but the compute
+        #   kernels that run meanwhile slow down by more than that)
         self._load_groups = 8  # groups (copies + events) per plan: copy/compute overlap vs per-copy cost
         mode = os.environ.get("WNW_OFFLOAD", "copy")
-        if mode not in ("copy", "device"):
-            raise ValueError(f"WNW_OFFLOAD must be 'copy' or 'device', got {mode!r}")
+        if mode not in ("copy", "staged", "device"):
+            raise ValueError(f"WNW_OFFLOAD must be 'copy', 'staged' or 'device', got {mode!r}")
         if mode == "device" and self.cpu_restore_k.shape[0] > 0 and \
                 not host_rows_readable(self.cpu_restore_k, self.cpu_restore_v):
             mode = "copy"  # the device cannot read these host rows: through the copy engines
         self._offload = mode
         self._h2d = None
+        self._stage = None
         self._staging_rows_hint = self._plan_rows_bound()
-        if mode == "copy" and self._staging_rows_hint > 0:
+        dt = self.cpu_restore_k.dtype
+        if mode == "staged" and self._staging_rows_hint > 0:
             # both pairs now, touched once: a first write into fresh pinned
             # pages is several times slower than the gathers that follow
-            dt = self.cpu_restore_k.dtype
             self._staging = [tuple(torch.zeros(self._staging_rows_hint, self.head_dim, dtype=dt, pin_memory=True)
                                    for _ in range(2)) for _ in range(2)]
+        elif mode == "copy" and self._staging_rows_hint > 0:
+            self._device_stage(self._staging_rows_hint)
         N = B * H
         self._plan_out = dict(
             load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
@@ -1119,10 +1135,10 @@ class WnWCache(FlatVarlenCache):
         bounds of each group and each layer's group.  Ranges are in transfer
         order (layer, sample, head, segment), so each layer's ranges are
         contiguous."""
-        lens = (ranges[:, 1] - ranges[:, 0]).to(torch.int64)
-        dst = torch.zeros(ranges.shape[0] + 1, dtype=torch.int64)
-        torch.cumsum(lens, 0, out=dst[1:])
-        ends = torch.searchsorted(dst, torch.cumsum(load_lens_2d.to(torch.int64).sum(dim=1), 0)).tolist()
+        r = ranges.numpy()
+        dst = np.zeros(r.shape[0] + 1, dtype=np.int64)
+        np.cumsum(r[:, 1].astype(np.int64) - r[:, 0], out=dst[1:])
+        ends = np.searchsorted(dst, np.cumsum(load_lens_2d.numpy().astype(np.int64).sum(axis=1))).tolist()
         bounds, group_of = [0], []
         for l0, l1 in self._group_layers():
             bounds.append(ends[l1 - 1])
@@ -1141,26 +1157,51 @@ class WnWCache(FlatVarlenCache):
         return [(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
 
     def _copy_loads(self, total: int, ranges: Tensor, load_lens_2d: Tensor) -> None:
-        """The plan's host ranges to the device through the transfer engine:
-        gathered into a pinned staging pair and copied by the DMA engines on
-        the transfer stream, group of layers by group, a layer's rebuild
-        waiting for its own group only.  Returns without waiting."""
+        """The plan's host ranges to the device through the transfer engine,
+        group of layers by group on the transfer stream, a layer's rebuild
+        waiting for its own group only: copied by the DMA engines straight
+        from the pinned restore rows into a device stage and put in transfer
+        order by a kernel ("copy"), or gathered by host threads into a pinned
+        staging pair that the DMA engines copy ("staged").  Returns without
+        waiting."""
         dev = self.device
         bounds, group_of = self._layer_groups(ranges, load_lens_2d)
-        stg_k, stg_v = self._engine_staging(total)
         stream = self._get_transfer_stream()
+        if self._h2d is None:
+            self._h2d = HostToDevice()
+        direct = self._offload == "copy"
         with torch.cuda.stream(stream):  # the copies into them follow on this stream
+            if direct:
+                stg_k, stg_v = self._device_stage(total)
             pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
             pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
         compute = torch.cuda.current_stream(dev)
         pk.record_stream(compute)
         pv.record_stream(compute)
-        if self._h2d is None:
-            self._h2d = HostToDevice()
-        self._h2d.start(self.cpu_restore_k, self.cpu_restore_v, ranges.to(torch.int32), bounds, stg_k, stg_v, pk, pv,
-                        stream)
+        if direct:
+            self._h2d.start_direct(self.cpu_restore_k, self.cpu_restore_v, ranges, bounds, stg_k, stg_v, pk, pv,
+                                   stream, check=False)
+        else:
+            stg_k, stg_v = self._engine_staging(total)
+            self._h2d.start(self.cpu_restore_k, self.cpu_restore_v, ranges.to(torch.int32), bounds, stg_k, stg_v,
+                            pk, pv, stream)
         self._pending_gpu_k, self._pending_gpu_v = pk, pv
         self._pending_layer_events = [("h2d", g) for g in group_of]
+
+    def _device_stage(self, rows: int) -> tuple[Tensor, Tensor]:
+        """The direct transfer's device stage (K and V rows, used on the
+        transfer stream only, where it is allocated): sized once by the bound
+        on a plan's rows, grown past it on demand (a new allocation on the
+        transfer stream, so the old rows stay untouched until the copies
+        queued before it are done)."""
+        if self._stage is None or self._stage[0].shape[0] < rows:
+            cap = max(rows, self._staging_rows_hint)
+            if self._stage is not None:
+                cap = max(cap, 2 * self._stage[0].shape[0])
+            dt = self.cpu_restore_k.dtype
+            with torch.cuda.stream(self._get_transfer_stream()):
+                self._stage = tuple(torch.empty(cap, self.head_dim, dtype=dt, device=self.device) for _ in range(2))
+        return self._stage
 
     def _plan_rows_bound(self) -> int:
         """An upper bound on the host rows one plan loads: per (layer, sample,

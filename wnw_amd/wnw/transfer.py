@@ -4,9 +4,12 @@ The offload channel of the reference (src/algorithms/wnw_cpp/code/
 planner.cpp:113-122 gathers a plan's host ranges into pinned staging;
 src/algorithms/wnw/code/cache.py:716-721, :868-881 copies the staging rows to
 the device on a side stream and waits for them before the rebuild), done by
-a background engine: worker threads gather the ranges group by group (groups
-of consecutive layers), each group is copied by the DMA engines as soon as it
-is gathered, and a layer waits only for its own group's copy.
+a background engine group by group (groups of consecutive layers), a layer
+waiting only for its own group's copy.  Two forms: ``start`` (worker threads
+gather the ranges into pinned staging, then the DMA engines copy each
+group) and ``start_direct`` (the DMA engines copy merged spans straight from
+the pinned host rows into a device stage, and a kernel puts the rows in
+transfer order).
 """
 from __future__ import annotations
 
@@ -63,6 +66,41 @@ class HostToDevice:
             self._h, _lib.ptr(host_k), _lib.ptr(host_v), host_k.shape[0], _lib.ptr(rg), rg.shape[0], gr,
             len(group_ranges) - 1, _lib.ptr(stg_k), _lib.ptr(stg_v), stg_k.shape[0], _lib.ptr(dev_k), _lib.ptr(dev_v),
             dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream)), "h2d start")
+
+    def start_direct(self, host_k: torch.Tensor, host_v: torch.Tensor, ranges: torch.Tensor,
+                     group_ranges: list[int], stage_k: torch.Tensor, stage_v: torch.Tensor, dev_k: torch.Tensor,
+                     dev_v: torch.Tensor, stream: torch.cuda.Stream, check: bool = True) -> None:
+        """``start`` without the host gather (``wnw_h2d_start_direct``): the
+        ranges are copied by the DMA engines straight from the pinned host
+        rows into ``stage_k`` / ``stage_v`` (device rows, in host order per
+        group, spans merged where ranges touch) and moved by a kernel on
+        ``stream`` into the same transfer-order rows of ``dev_k`` /
+        ``dev_v`` that ``start`` fills.  ``check=False`` skips the Python
+        checks for callers whose tensors are right by construction (the
+        library still checks every range and size)."""
+        if check:
+            for t in (host_k, host_v):
+                if t.device.type != "cpu" or not t.is_pinned() or not t.is_contiguous():
+                    raise _lib.WnwError("host rows must be contiguous pinned tensors")
+            if ranges.dtype != torch.int32 or ranges.device.type != "cpu" or ranges.dim() != 2 or \
+                    ranges.shape[1] != 2:
+                raise _lib.WnwError("ranges must be a CPU int32 [n, 2] tensor")
+            cur = torch.cuda.current_device()
+            for t in (stage_k, stage_v, dev_k, dev_v):
+                if not (t.is_cuda and t.device.index == cur and t.is_contiguous()):
+                    raise _lib.WnwError("stage and device rows must be contiguous tensors on the current device")
+            if host_k.shape != host_v.shape or stage_k.shape != stage_v.shape or dev_k.shape != dev_v.shape or \
+                    stage_k.shape[1:] != host_k.shape[1:] or dev_k.shape[1:] != host_k.shape[1:] or \
+                    len({host_k.dtype, host_v.dtype, stage_k.dtype, stage_v.dtype, dev_k.dtype, dev_v.dtype}) != 1:
+                raise _lib.WnwError("host, stage and device rows must have one row shape and dtype")
+        row_bytes = host_k.shape[1] * host_k.element_size()
+        rg = ranges.contiguous()
+        gr = (ctypes.c_int64 * len(group_ranges))(*group_ranges)
+        self._keep = (rg, gr)
+        _lib.check(_lib.lib().wnw_h2d_start_direct(
+            self._h, _lib.ptr(host_k), _lib.ptr(host_v), host_k.shape[0], _lib.ptr(rg), rg.shape[0], gr,
+            len(group_ranges) - 1, _lib.ptr(stage_k), _lib.ptr(stage_v), stage_k.shape[0], _lib.ptr(dev_k),
+            _lib.ptr(dev_v), dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream)), "h2d start_direct")
 
     def wait(self, group: int, stream: torch.cuda.Stream | None = None) -> None:
         """``stream`` (default: the current one) waits for group ``group``'s
