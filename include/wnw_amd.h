@@ -384,6 +384,56 @@ int wnw_fused_score_accumulate(const void* q, const void* k,
                                void* stream);
 
 /*
+ * Deferred class-A scoring (no reference counterpart as such: it splits
+ * q1_decode_attn_score, src/common/kv/fused_attn.py:68-156, over two
+ * launches so that no launch of its own is needed).  A streaming launch
+ * keeps the scaled logits of its flagged KV heads' audio rows and its final
+ * softmax normalisers in a score slot; the next streaming launch scores
+ * that slot into the accumulator while its own first loads are in flight
+ * (one 256-token slice of one sample per workgroup), exactly as
+ * wnw_decode_attn_score's scoring pass would (bit-identical sums).  A slot
+ * holds [n_seg, G, 2] normalisers then [n_seg, G, max_audio] logits, fp32
+ * (wnw_score_slot_bytes).
+ *
+ * wnw_decode_attn_append_deferred: wnw_decode_attn_append (the step's append
+ * into slack + attention, one launch) that also
+ *   - keeps this launch's logits and normalisers in keep_slot when keep_mask
+ *     ([num_kv_heads] non-zero = scored) is given (NOT scored yet), and
+ *   - scores prev_slot (kept by an earlier launch over segments prev_cu /
+ *     prev_base of prev_pool_rows rows; bit h of prev_kv_bits: KV head h
+ *     scored) into score_acc when prev_slot is given.
+ * audio_starts / audio_ends / max_audio / score_offsets / acc_len describe
+ * both launches.  Returns WNW_ENOTSUP, launching nothing, where the form
+ * does not apply (not the streaming kernel's case, more than 64 segments,
+ * more than 8 scored KV heads or 16 (scored KV head, query head) pairs, or
+ * more 256-token slices of the samples' audio than workgroups): the
+ * caller then scores with wnw_decode_attn_score_append /
+ * wnw_score_kept_logits.
+ * wnw_score_kept_logits: the scoring pass over a slot in a launch of its
+ * own (the last launch of a step has no next launch to carry it).
+ */
+int64_t wnw_score_slot_bytes(int64_t n_seg, int64_t group, int64_t max_audio);
+int wnw_decode_attn_append_deferred(
+    const void* q, void* k_pool, void* v_pool, const void* new_k,
+    const void* new_v, const int32_t* cu_old, int32_t* cu_new,
+    const int64_t* seg_base, const int32_t* seg_cap, int64_t n_seg,
+    int64_t group, int64_t head_dim, int64_t total_rows, int64_t pool_rows,
+    float scale, int dtype, void* out, int64_t num_kv_heads,
+    const int32_t* audio_starts, const int32_t* audio_ends, int64_t max_audio,
+    float* score_acc, const int32_t* score_offsets, int64_t acc_len,
+    const int32_t* keep_mask, float* keep_slot, uint64_t prev_kv_bits,
+    const float* prev_slot, const int32_t* prev_cu, const int64_t* prev_base,
+    int64_t prev_pool_rows, void* workspace, int64_t workspace_bytes,
+    void* stream);
+int wnw_score_kept_logits(const int32_t* kv_mask, const float* slot,
+                          const int32_t* cu, const int64_t* seg_base,
+                          int64_t kv_rows, int64_t n_seg, int64_t group,
+                          int64_t num_kv_heads, const int32_t* audio_starts,
+                          const int32_t* audio_ends, int64_t max_audio,
+                          float* score_acc, const int32_t* score_offsets,
+                          int64_t acc_len, void* stream);
+
+/*
  * Chunk scores and the top-k chunk choice of the decode planner, one launch
  * for every sample: the chunk selection of src/algorithms/wnw/code/
  * cache.py:632-649 (prefix-sum chunk means, topk) in the batched form of

@@ -35,6 +35,7 @@ def recording(cls):
     class Rec(cls):
         def decode_all_layers_done(self):
             if not torch.cuda.is_current_stream_capturing():
+                self._flush_pending_scores()  # the last deferred class-A scores of the step
                 self.rec_acc.append(self.score_accumulator.double().cpu().numpy().copy())
             return super().decode_all_layers_done()
 

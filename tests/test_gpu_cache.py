@@ -65,6 +65,7 @@ LAYOUTS = {"slack": dict(slack_rows=256), "tight": dict(slack_rows=3, tail=0), "
 @pytest.mark.parametrize("variant,fused,offload", [("wnw", True, "copy"), ("wnw", False, "copy"),
                                                    ("wnw_fallback", True, "copy"), ("wnw_cpp", True, "copy"),
                                                    ("wnw", True, "staged"), ("wnw_cpp", True, "staged"),
+                                                   ("wnw_nodefer", True, "copy"),
                                                    ("wnw", True, "device"), ("wnw_cpp", True, "device")])
 def test_decode_steps_match_simulation(variant, fused, offload, layout, monkeypatch):
     dev = torch.device("cuda", 0)
@@ -72,6 +73,9 @@ def test_decode_steps_match_simulation(variant, fused, offload, layout, monkeypa
     # rows into a device stage, or host gather threads into pinned staging
     # + DMA copies) or the device gather kernel reading pinned memory
     monkeypatch.setenv("WNW_OFFLOAD", offload)
+    # fused class-A scoring deferred to the next launch (default) or in a
+    # scoring pass of its own per layer
+    monkeypatch.setenv("WNW_DEFER_SCORES", "0" if variant == "wnw_nodefer" else "1")
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     cls = _recording(WnWCppCache if variant == "wnw_cpp" else WnWCache)

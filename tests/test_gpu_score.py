@@ -274,3 +274,134 @@ def test_fused_score_accumulate_many_samples():
     assert _lib.device_error() == 0
     ok, msg = allclose_report(acc.cpu().numpy().astype(np.float64), ref, S_ATOL, S_RTOL)
     assert ok, msg
+
+
+def _slack_layer(rng, lens, D, dtype, dev, slack=8):
+    """A pool with `slack` spare rows after each segment (slack layout):
+    (k pool, v pool, cu, seg_base, seg_cap) on the device and the host bits."""
+    n = len(lens)
+    cap = np.asarray(lens) + slack
+    base = np.concatenate([[0], np.cumsum(cap)[:-1]]).astype(np.int64)
+    rows = int(cap.sum()) + 64
+    k = rand_rows(rng, rows, D, dtype)
+    v = rand_rows(rng, rows, D, dtype)
+    t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
+    return dict(k=to_torch(k, dtype, dev), v=to_torch(v, dtype, dev), cu=t(cu_from_lens(lens)),
+                cu_out=torch.empty(n + 1, dtype=torch.int32, device=dev), base=t(base, torch.int64),
+                cap=t(cap.astype(np.int32)), rows=rows)
+
+
+def test_deferred_scoring_matches_the_scoring_pass():
+    """wnw_decode_attn_append_deferred over a sequence of layers (scored,
+    scored, not scored, scored, then the last slot scored on its own) gives
+    the same outputs, pools, offsets and accumulator bits as
+    q1_decode_attn_score's append form (attention + its own scoring pass)
+    layer by layer, and the accumulator matches the oracle."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(77)
+    H, G, D, B = 4, 4, 128, 4
+    n = B * H
+    dtype = "bfloat16"
+    a_s = [3, 0, 5, 1]
+    a_e = [900, 700, 1000, 650]
+    max_audio = max(e - s for s, e in zip(a_s, a_e))
+    offs = np.concatenate([[0], np.cumsum(np.array(a_e) - np.array(a_s))]).astype(np.int32)
+    masks = [[1, 0, 1, 0], [0, 1, 1, 0], None, [1, 1, 0, 1]]
+    t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
+    layers = []
+    for li in range(len(masks)):
+        lens = [int(x) for x in rng.integers(1000, 1400, n)]
+        layers.append(dict(lens=lens, q=rand_rows(rng, n * G, D, dtype).reshape(n, G, D),
+                           nk=rand_rows(rng, n, D, dtype), nv=rand_rows(rng, n, D, dtype), seed=int(rng.integers(1 << 30))))
+    acc0 = rng.random(int(offs[-1])).astype(np.float32)
+    scale = D ** -0.5
+
+    def run(deferred):
+        acc = torch.from_numpy(acc0.copy()).to(dev)
+        slots = [torch.empty(fused_attn.score_slot_bytes(n, G, max_audio) // 4, dtype=torch.float32, device=dev)
+                 for _ in range(2)]
+        outs, states, pending, turn = [], [], None, 0
+        for li, lay in enumerate(layers):
+            st = _slack_layer(np.random.default_rng(lay["seed"]), lay["lens"], D, dtype, dev)
+            q = to_torch(lay["q"], dtype, dev)
+            app = (to_torch(lay["nk"], dtype, dev), to_torch(lay["nv"], dtype, dev), st["cu_out"], st["cap"])
+            rows = sum(lay["lens"]) + n
+            mask = None if masks[li] is None else t(masks[li])
+            if not deferred:
+                if mask is None:
+                    out = fused_attn.decode_attn(q, st["k"], st["v"], st["cu"], scale, seg_base=st["base"],
+                                                 total_rows=rows, append=app)
+                else:
+                    out = fused_attn.q1_decode_attn_score(q, st["k"], st["v"], st["cu"], scale, mask, H, t(a_s),
+                                                          t(a_e), acc, t(offs), seg_base=st["base"], total_rows=rows,
+                                                          max_audio=max_audio, append=app)
+            else:
+                slot = slots[turn] if mask is not None else None
+                print(f"deferred layer {li}: keep={mask is not None} prev={pending is not None}", flush=True)
+                out = fused_attn.decode_attn_append_deferred(
+                    q, st["k"], st["v"], st["cu"], scale, seg_base=st["base"], total_rows=rows, append=app,
+                    num_kv_heads=H, audio_starts=t(a_s), audio_ends=t(a_e), max_audio=max_audio,
+                    score_accumulator=acc, score_offsets=t(offs), keep_mask=mask, keep_slot=slot, prev=pending)
+                assert out is not None, "the geometry is one the deferred form takes"
+                pending = (mask, slot, st["cu_out"], st["base"], st["rows"],
+                           sum(1 << h for h, f in enumerate(masks[li]) if f)) if mask is not None else None
+                if mask is not None:
+                    turn ^= 1
+            outs.append(out)
+            states.append(st)
+        if deferred and pending is not None:
+            fused_attn.score_kept_logits(pending, n, G, H, t(a_s), t(a_e), max_audio, acc, t(offs))
+        torch.cuda.synchronize()
+        assert _lib.device_error() == 0
+        return outs, states, acc
+
+    o1, s1, acc1 = run(False)
+    o2, s2, acc2 = run(True)
+    for li in range(len(layers)):
+        assert torch.equal(o1[li], o2[li]), f"output layer {li}"
+        for key in ("k", "v", "cu_out"):
+            assert torch.equal(s1[li][key], s2[li][key]), f"{key} layer {li}"
+    assert torch.equal(acc1, acc2), "accumulator bits"
+    # and the accumulator against the oracle (the appended segments)
+    ref = acc0.astype(np.float64)
+    for li, lay in enumerate(layers):
+        if masks[li] is None:
+            continue
+        st = s2[li]
+        kb = from_torch(st["k"], dtype)
+        cu2 = st["cu_out"].cpu().numpy()
+        ref = oracle.attn_scores(lay["q"], kb, cu2, scale, masks[li], H, a_s, a_e, offs, ref,
+                                 base=st["base"].cpu().numpy(), dtype=oracle.DT_BF16)
+    ok, msg = allclose_report(acc2.cpu().numpy().astype(np.float64), ref, S_ATOL, S_RTOL)
+    assert ok, msg
+
+
+def test_deferred_scoring_refuses_what_it_cannot_take():
+    """More than 64 segments: the deferred form launches nothing and says so
+    (None), leaving the output and the accumulator untouched."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(78)
+    H, G, D, B = 8, 4, 128, 9  # 72 segments
+    n = B * H
+    dtype = "bfloat16"
+    lens = [int(x) for x in rng.integers(200, 300, n)]
+    st = _slack_layer(rng, lens, D, dtype, dev)
+    t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
+    q = to_torch(rand_rows(rng, n * G, D, dtype).reshape(n, G, D), dtype, dev)
+    app = (to_torch(rand_rows(rng, n, D, dtype), dtype, dev), to_torch(rand_rows(rng, n, D, dtype), dtype, dev),
+           st["cu_out"], st["cap"])
+    acc = torch.zeros(B * 100, dtype=torch.float32, device=dev)
+    offs = t(np.arange(B + 1) * 100)
+    slots = [torch.empty(fused_attn.score_slot_bytes(n, G, 100) // 4, dtype=torch.float32, device=dev)
+             for _ in range(2)]
+    mask = t([1] + [0] * (H - 1))
+    out = torch.full((n, G, D), 7.0, dtype=torch.bfloat16, device=dev)
+    prev = (mask, slots[0], st["cu"], st["base"], st["rows"], 1)
+    got = fused_attn.decode_attn_append_deferred(
+        q, st["k"], st["v"], st["cu"], D ** -0.5, seg_base=st["base"], total_rows=sum(lens) + n, append=app,
+        num_kv_heads=H, audio_starts=t([0] * B), audio_ends=t([100] * B), max_audio=100, score_accumulator=acc,
+        score_offsets=offs, keep_mask=mask, keep_slot=slots[1], prev=prev, out=out)
+    torch.cuda.synchronize()
+    assert got is None
+    assert bool((out == 7.0).all()) and bool((acc == 0).all())
+    assert _lib.device_error() == 0

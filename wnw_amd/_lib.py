@@ -55,6 +55,11 @@ _SIGNATURES = {
     "wnw_fused_score_workspace_bytes": (_i64, [_i64, _i64]),
     "wnw_fused_score_accumulate": (_i32, [_vp] * 8 + [_i64] * 6 + [_f32, _i32, _vp, _i64, _vp]),
     "wnw_chunk_topk": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "wnw_score_slot_bytes": (_i64, [_i64, _i64, _i64]),
+    "wnw_decode_attn_append_deferred": (_i32, [_vp] * 9 + [_i64] * 5 + [_f32, _i32, _vp, _i64, _vp, _vp, _i64, _vp,
+                                                                      _vp, _i64, _vp, _vp, ctypes.c_uint64]
+                                        + [_vp] * 3 + [_i64, _vp, _i64, _vp]),
+    "wnw_score_kept_logits": (_i32, [_vp, _vp, _vp, _vp] + [_i64] * 4 + [_vp, _vp, _i64, _vp, _vp, _i64, _vp]),
     "wnw_read_stream": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp]),
     # host planner (CPU only)
     "wnw_planner_create": (_vp, [_i32, _i32, _i32, _i32]),

@@ -52,6 +52,7 @@
 namespace wnw {
 
 static constexpr int kMaxGroup = 16;
+static constexpr int kMaxGroupPrev = 8;  // query heads per KV head of the deferred scoring (the streaming kernel's limit)
 static constexpr int kRing = 64;  // LDS cache of segment bounds per workgroup
 static constexpr float kNegBig = -1e30f;
 static constexpr float kLog2e = 1.4426950408889634f;
@@ -89,7 +90,155 @@ struct AttnParams {
   const void* new_v;
   int32_t* cu_out;     // [n_seg + 1], must not alias cu
   const int32_t* cap;  // [n_seg]
+  // Streaming kernel, direct table only, null otherwise: a previous launch's
+  // kept logits (pv_xlog) and normalisers (pv_lse), scored into the class-A
+  // accumulator by this launch (AttnPrevScore); audio_s / audio_e /
+  // max_audio / Hkv above describe both launches.  Workgroup i takes the
+  // 256 tokens of slice i = (sample, block of 256 audio tokens).
+  const float* pv_xlog;
+  const float* pv_lse;
+  uint64_t pv_kvlist;  // the KV heads that launch scored, ascending, 8 bits each (pv_nkv of them)
+  int32_t pv_nkv;
+  const int32_t* pv_cu;
+  const int64_t* pv_base;
+  int64_t pv_kv_rows;
+  float* pv_acc;
+  const int32_t* pv_acc_off;
+  int64_t pv_acc_len;
+  int32_t pv_nblk;  // 256-token blocks per sample
+  int32_t pv_slices;  // samples x pv_nblk (<= the grid)
 };
+
+// Deferred scoring of the previous launch's kept logits.  Workgroup i < the
+// slice count takes slice i = (sample b, block of 256 audio tokens), one
+// token per thread; the other workgroups load slice 0's data and store
+// nothing.  The sample's audio range and accumulator offset are loaded at
+// the start, beside the segment table; the rest after the stream (done
+// earlier, the loads cost the stream more than they save): lane l < 16
+// pair l's normalisers (pair = (flagged KV head i, query head g),
+// l = i * G + g), lane 16 + i the bounds of flagged KV head i's segment,
+// every thread its token's logits for all pairs and its accumulator entry,
+// all in one round trip.  The weights exp2(x - max) / sum are summed over
+// each segment's heads, then over the segments, then added to the
+// accumulator entry -- logit_score_kernel's order and validity rules, so
+// the sums are bit-identical to that pass; the entry is stored at the end
+// of the launch.
+static constexpr int kPrevLogits = 16;  // pairs per sample the deferred form takes (<= 8 KV heads)
+struct PrevLoads {
+  float x[kPrevLogits];
+  float m, l;           // lane < 16: pair `lane`'s normalisers
+  int32_t c0, c1;       // lane 16 + i: flagged KV head i's segment offsets
+  int64_t bv;           //   ... and physical first row
+  int32_t a0, a1, off;  // the sample's audio range and accumulator offset
+  float prior;          // the token's accumulator entry
+  // the entry's address, and whether it is stored (bit 0), the offset is
+  // valid (bit 1), the workgroup has a slice (bit 2), the slice is its
+  // sample's first (bit 3)
+  float* dst;
+  int32_t flags;
+};
+
+__device__ __forceinline__ int prev_slice(const AttnParams& p) {
+  return (int32_t)blockIdx.x < p.pv_slices ? (int)blockIdx.x : 0;
+}
+
+__device__ __forceinline__ void prev_issue_head(const AttnParams& p, PrevLoads& pl) {
+  const int b = prev_slice(p) / p.pv_nblk;
+  pl.a0 = p.audio_s[b];
+  pl.a1 = p.audio_e[b];
+  pl.off = p.pv_acc_off[b];
+}
+
+__device__ __forceinline__ void prev_issue_body(const AttnParams& p, int tid, PrevLoads& pl) {
+  const int lane = tid & 63;
+  const int nb = p.pv_nblk, G = p.G, nkv = p.pv_nkv, Hkv = p.Hkv;
+  const int sl = prev_slice(p);
+  const int b = sl / nb, blk = sl - b * nb;
+  const int np = nkv * G;
+  {
+    const int t = min(lane, np - 1), i = t / G, g = t - i * G;
+    const int s = b * Hkv + (int)((p.pv_kvlist >> (8 * i)) & 0xff);
+    pl.m = p.pv_lse[((int64_t)s * G + g) * 2];
+    pl.l = p.pv_lse[((int64_t)s * G + g) * 2 + 1];
+  }
+  {
+    const int i = min(max(lane - 16, 0), nkv - 1);
+    const int s = b * Hkv + (int)((p.pv_kvlist >> (8 * i)) & 0xff);
+    pl.c0 = p.pv_cu[s];
+    pl.c1 = p.pv_cu[s + 1];
+    pl.bv = p.pv_base ? p.pv_base[s] : 0;
+  }
+  const int64_t jc = min((int64_t)blk * 256 + tid, p.max_audio - 1);
+#pragma unroll
+  for (int t = 0; t < kPrevLogits; ++t) {
+    const int tc = min(t, np - 1), i = tc / G, g = tc - i * G;  // uniform
+    const int s = b * Hkv + (int)((p.pv_kvlist >> (8 * i)) & 0xff);
+    pl.x[t] = p.pv_xlog[((int64_t)s * G + g) * p.max_audio + jc];
+  }
+  // the entry, clamped into the accumulator (a bad offset is refused later)
+  const int off = __builtin_amdgcn_readfirstlane(pl.off);
+  float* dst = p.pv_acc + min(max((int64_t)off + jc, (int64_t)0), p.pv_acc_len - 1);
+  pl.prior = *dst;
+  pl.dst = dst;
+  const int n_audio = pl.a1 - pl.a0;
+  const int64_t j = (int64_t)blk * 256 + tid;
+  const bool off_ok = off >= 0 && (int64_t)off + n_audio <= p.pv_acc_len;
+  const bool has_slice = (int32_t)blockIdx.x < p.pv_slices;
+  pl.flags = ((has_slice && off_ok && j < n_audio && j < p.max_audio) ? 1 : 0) | (off_ok ? 2 : 0) |
+             (has_slice ? 4 : 0) | (blk == 0 ? 8 : 0);
+}
+
+// The token's accumulator entry (at, -1: none) and its new value, from
+// loads that have arrived.
+__device__ __forceinline__ void prev_finish(const AttnParams& p, int tid, const PrevLoads& pl, float*& dst,
+                                            float& total) {
+  dst = nullptr;
+  total = 0.f;
+  const int flags = __builtin_amdgcn_readfirstlane(pl.flags);  // bits 1, 2, 3 are uniform
+  if (!(flags & 4)) return;  // uniform: slice 0's data, loaded for the wait counts only
+  if (!(flags & 2)) {  // the accumulator cannot hold the sample's tokens
+    if (tid == 0 && (flags & 8)) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+    return;
+  }
+  const int G = p.G, nkv = p.pv_nkv;
+  const bool has_base = p.pv_base != nullptr;
+  // flagged segments whose rows cover the audio range (the others are
+  // skipped and reported, as the scoring pass does)
+  uint32_t use = 0;
+  for (int i = 0; i < nkv; ++i) {
+    const int32_t c0 = __builtin_amdgcn_readlane(pl.c0, 16 + i), c1 = __builtin_amdgcn_readlane(pl.c1, 16 + i);
+    const uint32_t blo = __builtin_amdgcn_readlane((uint32_t)pl.bv, 16 + i);
+    const uint32_t bhi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)pl.bv >> 32), 16 + i);
+    const int64_t len = (int64_t)c1 - c0;
+    const int64_t base = has_base ? (int64_t)(((uint64_t)bhi << 32) | blo) : (int64_t)c0;
+    const bool oob = (pl.a0 < 0) | (pl.a1 > len) | (base < 0) | (base + len > p.pv_kv_rows);
+    if (!oob) use |= 1u << i;
+    else if (tid == 0 && blockIdx.x == 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
+  }
+  // lane t holds pair t's normaliser: its reciprocal once per lane, not
+  // once per pair and thread
+  const float inv_lane = 1.f / pl.l;
+  float sum = 0.f, sc = 0.f;
+#pragma unroll
+  for (int t = 0; t < kPrevLogits; ++t) {
+    const int i = t / G, g = t - i * G;  // uniform
+    if (i < nkv) {
+      const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.m), t));
+      const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_lane), t));
+      // v_exp_f32 directly, as the scoring pass: arguments are <= 0 and
+      // weights below 2^-126 (flushed to zero) are negligible
+      if ((use >> i) & 1) sc += __builtin_amdgcn_exp2f(pl.x[t] - m) * inv;
+      if (g == G - 1) {
+        sum += sc;
+        sc = 0.f;
+      }
+    }
+  }
+  if (pl.flags & 1) {
+    dst = pl.dst;
+    total = pl.prior + sum;
+  }
+}
 
 // A segment is attended when its rows fit both row spaces; every piece of
 // logic that decides this (owner outputs, pieces, the stream walk) uses this
@@ -1007,7 +1156,10 @@ struct SStep {
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
 // APPEND: append new_k / new_v[s] to every segment first (fused append).
-template <typename T, int D, int NW, int QD, bool XL, bool APPEND, bool DIRECT>
+// PV: score the previous launch's kept logits (deferred scoring; direct
+// table and fused append only), an instance of its own so that the other
+// launches carry none of its code or argument loads.
+template <typename T, int D, int NW, int QD, bool XL, bool APPEND, bool DIRECT, bool PV = false>
 // The fields read first lead the argument list as scalars: the build asks
 // for 16 preloaded argument dwords (-amdgpu-kernarg-preload-count), of which
 // the hardware delivers 14 in SGPRs at dispatch (the other two user SGPRs
@@ -1051,6 +1203,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   p.split_inv = inv_arg;
   p.n_seg = nseg_arg;
   p.G = g_arg;
+  // deferred scoring: the sample's audio range and accumulator offset,
+  // loaded beside the segment table
+  PrevLoads pl;
+  static_assert(!PV || (DIRECT && APPEND), "deferred scoring rides in the direct, fused-append instances");
+  if constexpr (PV) prev_issue_head(p, pl);
   using G_ = StreamGeom<D>;
   using Ops = StreamOps<T>;
   constexpr int NT = NW * 64;
@@ -1526,6 +1683,15 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     if (!hA) break;
   }
   wait_vmcnt<0>();
+  // deferred scoring, after the stream: every load of the stream is in, so
+  // the compiler's wait counts for these loads hold (it does not count the
+  // stream's own loads); the accumulator entry is stored at the very end
+  float* pv_dst = nullptr;
+  float pv_total = 0.f;
+  if constexpr (PV) {
+    prev_issue_body(p, tid, pl);
+    prev_finish(p, tid, pl, pv_dst, pv_total);
+  }
 
   // ---- shared pieces: merge the waves' states through LDS
   __syncthreads();  // every wave is done with its step buffers (reused below)
@@ -1720,6 +1886,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       if (!lneg && llen + 1 > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
     }
   }
+  if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
 }
 
 // ---------------------------------------------------------------------------
@@ -1943,16 +2110,16 @@ static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex&
 // Streaming kernel launch: QD = q loads per step, dynamic LDS as sized by
 // stream_lds_bytes (above 64 KB, so the limit is raised once per instance
 // and device).
-template <typename T, int D, int QD, bool XL, bool APPEND, bool DIRECT>
+template <typename T, int D, int QD, bool XL, bool APPEND, bool DIRECT, bool PV = false>
 static hipError_t launch_stream_k(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
   const int lds = stream_lds_bytes(D, kNW, stream_qslot(ap.G, D, APPEND), APPEND);
   static std::mutex mu;
   static std::vector<signed char> done;
   const hipError_t attr_err =
-      set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT>,
+      set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT, PV>,
                          stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND));
   if (attr_err != hipSuccess) return attr_err;
-  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
+  hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT, PV>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
                      st, ap.cu, ap.base, ap.cap, ap.q, ap.k, ap.v, ap.n_seg,
                      (int32_t)((uint32_t)ap.G | ((uint32_t)n_wg << 8)), ap.split_inv, ap);
   return hipGetLastError();
@@ -1962,6 +2129,10 @@ static hipError_t launch_stream_k(const AttnParams& ap, int64_t n_wg, hipStream_
 // segment); more take the workgroup scheduling pass.
 template <typename T, int D, int QD, bool XL, bool APPEND>
 static hipError_t launch_stream(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
+  if constexpr (APPEND) {
+    if (ap.pv_xlog)  // the host allows it with the direct table only
+      return ap.n_seg <= 64 ? launch_stream_k<T, D, QD, XL, APPEND, true, true>(ap, n_wg, st) : hipErrorInvalidValue;
+  }
   return ap.n_seg <= 64 ? launch_stream_k<T, D, QD, XL, APPEND, true>(ap, n_wg, st)
                         : launch_stream_k<T, D, QD, XL, APPEND, false>(ap, n_wg, st);
 }
@@ -2063,7 +2234,7 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
                      const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc,
-                     const AttnAppend* app) {
+                     const AttnAppend* app, const AttnPrevScore* prev) {
   if (logits_kept) *logits_kept = 0;
   WNW_CHECK_ARG(n_seg >= 0 && n_seg < (1ll << 30), "n_seg out of range: %lld", (long long)n_seg);
   if (n_seg == 0) return WNW_OK;
@@ -2151,6 +2322,64 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
   ap.new_k = ap.new_v = nullptr;
   ap.cu_out = nullptr;
   ap.cap = nullptr;
+  ap.pv_xlog = ap.pv_lse = nullptr;
+  ap.pv_kvlist = 0;
+  ap.pv_nkv = 0;
+  ap.pv_slices = 0;
+  ap.pv_cu = ap.pv_acc_off = nullptr;
+  ap.pv_base = nullptr;
+  ap.pv_acc = nullptr;
+  ap.pv_kv_rows = ap.pv_acc_len = 0;
+  ap.pv_nblk = 0;
+  if (prev) {
+    // deferred scoring rides in the streaming kernel's direct-table form
+    // only, one slice of 256 tokens per workgroup: elsewhere the caller
+    // scores the slot in its own launch
+    WNW_CHECK_ARG(prev->xlog && prev->lse && prev->cu && prev->acc && prev->acc_off && prev->audio_s &&
+                      prev->audio_e,
+                  "null deferred-scoring argument");
+    WNW_CHECK_ARG(prev->hkv >= 1 && n_seg % prev->hkv == 0 && prev->max_audio > 0 && prev->kv_rows >= 0 &&
+                      prev->acc_len >= 0,
+                  "bad deferred-scoring geometry");
+    const int64_t nblk = (prev->max_audio + 255) / 256;
+    int nkv = 0;
+    uint64_t kvlist = 0;
+    for (int h = 0; h < prev->hkv && h < 64; ++h)
+      if ((prev->kv_bits >> h) & 1) {
+        if (nkv < 8) kvlist |= (uint64_t)h << (8 * nkv);
+        ++nkv;
+      }
+    WNW_CHECK_ARG(prev->hkv <= 64 && (prev->hkv == 64 || (prev->kv_bits >> prev->hkv) == 0),
+                  "deferred-scoring KV heads outside [0, %d)", prev->hkv);
+    if (kern != WNW_ATTN_STREAM || n_seg > 64 || nkv > 8 || nkv * group > kPrevLogits ||
+        (n_seg / prev->hkv) * nblk > P) {
+      set_error("deferred scoring needs the streaming kernel, at most 64 segments, at most 8 scored KV heads "
+                "and %d (KV head, query head) pairs, and one 256-token slice per workgroup (%lld slices, %lld "
+                "workgroups)",
+                kPrevLogits, (long long)((n_seg / prev->hkv) * nblk), (long long)P);
+      return WNW_ENOTSUP;
+    }
+    if (logits && kern == WNW_ATTN_STREAM)
+      WNW_CHECK_ARG(logits->hkv == prev->hkv && logits->max_audio == prev->max_audio &&
+                        logits->audio_s == prev->audio_s && logits->audio_e == prev->audio_e,
+                    "the deferred scoring and this launch's logits must share the audio geometry");
+    ap.pv_xlog = nkv > 0 ? prev->xlog : nullptr;  // nothing scored: nothing to do
+    ap.pv_lse = prev->lse;
+    ap.pv_kvlist = kvlist;
+    ap.pv_nkv = nkv;
+    ap.pv_slices = (int32_t)((n_seg / prev->hkv) * nblk);
+    ap.pv_cu = prev->cu;
+    ap.pv_base = prev->base;
+    ap.pv_kv_rows = prev->kv_rows;
+    ap.pv_acc = prev->acc;
+    ap.pv_acc_off = prev->acc_off;
+    ap.pv_acc_len = prev->acc_len;
+    ap.pv_nblk = (int32_t)nblk;
+    ap.audio_s = prev->audio_s;
+    ap.audio_e = prev->audio_e;
+    ap.max_audio = prev->max_audio;
+    ap.Hkv = prev->hkv;
+  }
   hipStream_t st = (hipStream_t)stream;
   if (app) {
     if (kern == WNW_ATTN_STREAM) {  // fused into the launch

@@ -266,7 +266,9 @@ __global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(
       const int t = t0 + u;
       if (t < nt) {
         const int i = t / G, g = t - i * G;
-        sc += exp2f(x[u] - m_sh[i * kLogitG + g]) * inv_sh[i * kLogitG + g];
+        // v_exp_f32 directly: arguments are <= 0 (m is the maximum) and
+        // weights below 2^-126 (flushed to zero) are negligible
+        sc += __builtin_amdgcn_exp2f(x[u] - m_sh[i * kLogitG + g]) * inv_sh[i * kLogitG + g];
         if (g == G - 1) {
           total += sc;
           sc = 0.f;
@@ -596,6 +598,115 @@ extern "C" int wnw_decode_attn_score_append(
   return decode_attn_score_impl(q, k_pool, v_pool, cu_old, seg_base, n_seg, group, head_dim, total_rows, pool_rows,
                                 scale, dtype, out, ca_kv_mask, num_kv_heads, audio_starts, audio_ends, score_acc,
                                 score_offsets, acc_len, max_audio, workspace, workspace_bytes, stream, &app);
+}
+
+// ---------------------------------------------------------------------------
+// deferred scoring: score slots handed from one streaming launch to the next
+// ---------------------------------------------------------------------------
+// A slot holds one launch's final normalisers [n_seg, G, 2] and its kept
+// logits [n_seg, G, max_audio] (fp32, 256-byte aligned parts).
+static int64_t slot_logits_offset(int64_t n_seg, int64_t group) { return up256(n_seg * group * 2 * 4); }
+
+extern "C" int64_t wnw_score_slot_bytes(int64_t n_seg, int64_t group, int64_t max_audio) {
+  if (n_seg < 0 || group <= 0 || max_audio < 0) return -1;
+  return slot_logits_offset(n_seg, group) + up256(n_seg * group * max_audio * 4);
+}
+
+// The logit pass over a slot (the scores of a launch that kept them and had
+// no later launch to carry them).
+extern "C" int wnw_score_kept_logits(const int32_t* kv_mask, const float* slot, const int32_t* cu,
+                                     const int64_t* seg_base, int64_t kv_rows, int64_t n_seg, int64_t group,
+                                     int64_t num_kv_heads, const int32_t* audio_starts, const int32_t* audio_ends,
+                                     int64_t max_audio, float* score_acc, const int32_t* score_offsets,
+                                     int64_t acc_len, void* stream) {
+  WNW_CHECK_ARG(kv_mask && slot && cu && audio_starts && audio_ends && score_acc && score_offsets,
+                "null pointer argument");
+  WNW_CHECK_ARG(n_seg >= 0 && group >= 1 && group <= kLogitG && num_kv_heads >= 1 && num_kv_heads <= kLogitKv &&
+                    n_seg % num_kv_heads == 0,
+                "bad geometry: n_seg %lld, group %lld, num_kv_heads %lld", (long long)n_seg, (long long)group,
+                (long long)num_kv_heads);
+  WNW_CHECK_ARG(max_audio >= 0 && acc_len >= 0 && kv_rows >= 0, "negative size");
+  WNW_CHECK_ARG(n_seg / num_kv_heads <= 65535, "at most 65535 samples (the scoring grid's y extent)");
+  if (n_seg == 0 || max_audio == 0) return WNW_OK;
+  LogitScoreParams lp;
+  lp.xlog = slot + slot_logits_offset(n_seg, group) / 4;
+  lp.acc_off = score_offsets;
+  lp.acc = score_acc;
+  lp.err = device_error_word();
+  lp.kv_rows = kv_rows;
+  lp.acc_len = acc_len;
+  lp.max_audio = max_audio;
+  const int32_t hg = (int32_t)num_kv_heads | ((int32_t)group << 16);
+  const dim3 grid((unsigned)((max_audio + kLogitThreads - 1) / kLogitThreads), (unsigned)(n_seg / num_kv_heads));
+  hipLaunchKernelGGL(logit_score_kernel, grid, dim3(kLogitThreads), 0, (hipStream_t)stream, audio_starts, audio_ends,
+                     kv_mask, cu, seg_base, slot, hg, (int32_t)n_seg, lp);
+  WNW_CHECK_HIP(hipGetLastError(), "logit score launch");
+  return WNW_OK;
+}
+
+extern "C" int wnw_decode_attn_append_deferred(
+    const void* q, void* k_pool, void* v_pool, const void* new_k, const void* new_v, const int32_t* cu_old,
+    int32_t* cu_new, const int64_t* seg_base, const int32_t* seg_cap, int64_t n_seg, int64_t group,
+    int64_t head_dim, int64_t total_rows, int64_t pool_rows, float scale, int dtype, void* out,
+    int64_t num_kv_heads, const int32_t* audio_starts, const int32_t* audio_ends, int64_t max_audio,
+    float* score_acc, const int32_t* score_offsets, int64_t acc_len, const int32_t* keep_mask, float* keep_slot,
+    uint64_t prev_kv_bits, const float* prev_slot, const int32_t* prev_cu, const int64_t* prev_base,
+    int64_t prev_pool_rows, void* workspace, int64_t workspace_bytes, void* stream) {
+  WNW_CHECK_ARG(num_kv_heads >= 1 && num_kv_heads <= kLogitKv && n_seg % num_kv_heads == 0,
+                "n_seg (%lld) must be a multiple of num_kv_heads (%lld), at most %d KV heads", (long long)n_seg,
+                (long long)num_kv_heads, kLogitKv);
+  WNW_CHECK_ARG((keep_mask == nullptr) == (keep_slot == nullptr), "the keep mask and its slot come together");
+  WNW_CHECK_ARG(!(keep_slot && prev_slot) || (const float*)keep_slot != prev_slot,
+                "this launch's slot must not be the slot it scores");
+  WNW_CHECK_ARG(max_audio > 0 || (!keep_mask && !prev_slot), "scoring needs max_audio > 0");
+  WNW_CHECK_ARG(!prev_slot || (prev_cu && acc_len > 0), "the scored slot needs its offsets and an accumulator");
+  // the kept logits need the streaming kernel (the only one that keeps them)
+  if ((keep_mask || prev_slot) &&
+      !((dtype == WNW_BF16 || dtype == WNW_F16) && (head_dim == 64 || head_dim == 128) && group <= kLogitG)) {
+    set_error("deferred scoring needs the streaming kernel (bf16/f16, head_dim 64 or 128, group <= %d)", kLogitG);
+    return WNW_ENOTSUP;
+  }
+  AttnAppend app;
+  app.new_k = new_k;
+  app.new_v = new_v;
+  app.cu_out = cu_new;
+  app.cap = seg_cap;
+  AttnLogits lg;
+  if (keep_mask) {
+    WNW_CHECK_ARG(audio_starts && audio_ends, "null audio range");
+    lg.xlog = keep_slot + slot_logits_offset(n_seg, group) / 4;
+    lg.mask = keep_mask;
+    lg.audio_s = audio_starts;
+    lg.audio_e = audio_ends;
+    lg.max_audio = max_audio;
+    lg.hkv = (int32_t)num_kv_heads;
+  }
+  AttnPrevScore pv;
+  if (prev_slot) {
+    pv.lse = prev_slot;
+    pv.xlog = prev_slot + slot_logits_offset(n_seg, group) / 4;
+    pv.kv_bits = prev_kv_bits;
+    pv.cu = prev_cu;
+    pv.base = prev_base;
+    pv.kv_rows = prev_pool_rows;
+    pv.acc = score_acc;
+    pv.acc_off = score_offsets;
+    pv.acc_len = acc_len;
+    pv.audio_s = audio_starts;
+    pv.audio_e = audio_ends;
+    pv.max_audio = max_audio;
+    pv.hkv = (int32_t)num_kv_heads;
+  }
+  int kept = 0;
+  const int rc = decode_attn_impl(q, k_pool, v_pool, cu_old, seg_base, n_seg, group, head_dim, total_rows, pool_rows,
+                                  scale, dtype, out, workspace, workspace_bytes, WNW_ATTN_STREAM, 0,
+                                  keep_mask ? keep_slot : nullptr, keep_mask ? &lg : nullptr, &kept, stream, false,
+                                  &app, prev_slot ? &pv : nullptr);
+  if (rc == WNW_OK && keep_mask && !kept) {  // cannot happen with the streaming kernel
+    set_error("the logits were not kept");
+    return WNW_EHIP;
+  }
+  return rc;
 }
 
 extern "C" int64_t wnw_fused_score_workspace_bytes(int64_t n_samples, int64_t n_heads) {

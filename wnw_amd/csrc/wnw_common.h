@@ -41,6 +41,25 @@ struct AttnAppend {
   const int32_t* cap;  // [n_seg] rows each segment may occupy from its base
 };
 
+// Deferred class-A scoring: the logits and normalisers a previous streaming
+// launch kept (a score slot), scored by the next streaming launch while its
+// first loads are in flight.  Rules as logit_score_kernel's.
+struct AttnPrevScore {
+  const float* lse;        // [n_seg, G, 2] final (max, sum), log2 domain
+  const float* xlog;       // [n_seg, G, max_audio]
+  uint64_t kv_bits;        // bit h: KV head h scored by that launch
+  const int32_t* cu;       // [n_seg + 1] its offsets after its append
+  const int64_t* base;     // [n_seg] its physical first rows (or null: cu)
+  int64_t kv_rows;         // its pool rows
+  float* acc;              // class-A accumulator, acc_off [B + 1], acc_len entries
+  const int32_t* acc_off;
+  int64_t acc_len;
+  const int32_t* audio_s;  // [B]
+  const int32_t* audio_e;
+  int64_t max_audio;
+  int32_t hkv;
+};
+
 // Shared by the public attention entry points; lse (optional) receives each
 // segment's final softmax (max, sum) in the log2 domain, [n_seg, G, 2].
 // logits (optional) is honoured by the streaming kernel only; *logits_kept
@@ -52,7 +71,7 @@ int decode_attn_impl(const void* q, const void* k, const void* v, const int32_t*
                      int64_t total_rows, int64_t kv_rows, float scale, int dtype, void* out,
                      void* workspace, int64_t workspace_bytes, int kernel, int64_t n_wg, float* lse,
                      const AttnLogits* logits, int* logits_kept, void* stream, bool noalloc,
-                     const AttnAppend* app);
+                     const AttnAppend* app, const AttnPrevScore* prev = nullptr);
 
 #define WNW_CHECK_ARG(cond, ...)       \
   do {                                 \

@@ -265,6 +265,62 @@ def q1_decode_attn_score(
     return out
 
 
+def score_slot_bytes(nseg: int, group: int, max_audio: int) -> int:
+    """Bytes of one score slot (``wnw_score_slot_bytes``): a launch's final
+    softmax normalisers and the logits of its scored audio rows."""
+    n = int(_lib.lib().wnw_score_slot_bytes(nseg, group, max_audio))
+    if n < 0:
+        raise _lib.WnwError("bad score slot geometry")
+    return n
+
+
+def decode_attn_append_deferred(q_flat, k_pool, v_pool, cu_k, scale, *, seg_base, total_rows, append, num_kv_heads,
+                                audio_starts, audio_ends, max_audio, score_accumulator, score_offsets,
+                                keep_mask=None, keep_slot=None, prev=None, out=None, workspace=None):
+    """The step's in-place append + attention in one launch
+    (``wnw_decode_attn_append_deferred``) that keeps this launch's class-A
+    logits and normalisers in ``keep_slot`` (KV heads ``keep_mask``; not
+    scored yet) and scores an earlier launch's slot ``prev`` = (mask, slot,
+    cu, seg_base, pool_rows, kv_bits) into the accumulator (``kv_bits``: bit h
+    set when KV head h was scored, the host's copy of ``mask``), as the second half of the
+    reference's ``q1_decode_attn_score`` (src/common/kv/fused_attn.py:
+    68-156) split over two launches.  Returns the output [nseg, G, D], or
+    None, launching nothing, where this form does not apply (the caller then
+    scores another way).  The caller's tensors are trusted (the cache's own:
+    dtypes, devices and shapes checked where they are made); the library
+    checks sizes and every offset it follows."""
+    nseg, g, d = q_flat.shape
+    if out is None:
+        out = torch.empty(nseg, g, d, device=q_flat.device, dtype=q_flat.dtype)
+    ws = workspace if workspace is not None else workspace_for(q_flat.device)
+    buf, nbytes = ws.get(nseg, g, d)
+    new_k, new_v, cu_new, seg_cap = append
+    _pm, ps, pcu, pbase, prows, pbits = prev if prev is not None else (None, None, None, None, 0, 0)
+    rc = _lib.lib().wnw_decode_attn_append_deferred(
+        _lib.ptr(q_flat), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(new_k), _lib.ptr(new_v), _lib.ptr(cu_k),
+        _lib.ptr(cu_new), _lib.ptr(seg_base), _lib.ptr(seg_cap), nseg, g, d, int(total_rows), k_pool.shape[0],
+        float(scale), _lib.dtype_code(q_flat.dtype), _lib.ptr(out), int(num_kv_heads), _lib.ptr(audio_starts),
+        _lib.ptr(audio_ends), int(max_audio), _lib.ptr(score_accumulator), _lib.ptr(score_offsets),
+        score_accumulator.numel(), _lib.ptr(keep_mask), _lib.ptr(keep_slot), int(pbits), _lib.ptr(ps),
+        _lib.ptr(pcu), _lib.ptr(pbase), int(prows), _lib.ptr(buf), nbytes, _lib.stream_of(q_flat.device))
+    if rc == _lib.WNW_ENOTSUP:
+        return None
+    _lib.check(rc, "decode_attn_append_deferred")
+    return out
+
+
+def score_kept_logits(prev, nseg: int, group: int, num_kv_heads: int, audio_starts, audio_ends, max_audio: int,
+                      score_accumulator, score_offsets) -> None:
+    """The scoring pass over a slot ``prev`` = (mask, slot, cu, seg_base,
+    pool_rows, kv_bits) in a launch of its own (``wnw_score_kept_logits``)."""
+    pm, ps, pcu, pbase, prows, _bits = prev
+    _lib.check(_lib.lib().wnw_score_kept_logits(
+        _lib.ptr(pm), _lib.ptr(ps), _lib.ptr(pcu), _lib.ptr(pbase), int(prows), nseg, group, int(num_kv_heads),
+        _lib.ptr(audio_starts), _lib.ptr(audio_ends), int(max_audio), _lib.ptr(score_accumulator),
+        _lib.ptr(score_offsets), score_accumulator.numel(), _lib.stream_of(score_accumulator.device)),
+        "score_kept_logits")
+
+
 def _check_score(q_flat, k_flat, v_flat, cu_k, ca_kv_mask, num_kv_heads, audio_starts, audio_ends,
                  score_accumulator, score_offsets, seg_base, total_rows):
     """Validate q1_decode_attn_score's tensors; returns the ones the launch

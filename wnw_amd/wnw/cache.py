@@ -69,7 +69,8 @@ from torch import Tensor
 
 from .. import _lib
 from ..kv.flat_cache import FlatVarlenCache
-from ..kv.fused_attn import decode_attn, q1_decode_attn, q1_decode_attn_score
+from ..kv.fused_attn import (decode_attn, decode_attn_append_deferred, q1_decode_attn, q1_decode_attn_score,
+                             score_kept_logits, score_slot_bytes)
 from ..kv.kernels import append_inplace, interleave_append_kv
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
@@ -684,7 +685,7 @@ class WnWCache(FlatVarlenCache):
         self._empty_i32 = torch.empty(0, dtype=torch.int32, device=self.device)
         G = self.num_kv_groups
         self._decode_after_groups = [[] for _ in range(self.num_layers)]
-        self._layer_foldable, self._ca_kv_mask_by_layer = [], []
+        self._layer_foldable, self._ca_kv_mask_by_layer, self._ca_kv_bits_by_layer = [], [], []
         self._decode_class_a_local = None
         for l in range(self.num_layers):
             ca = self.config.get_layer_class_a(l)
@@ -705,8 +706,19 @@ class WnWCache(FlatVarlenCache):
                 self._ca_kv_mask_by_layer.append(mask.to(self.device))
             else:
                 self._ca_kv_mask_by_layer.append(None)
+            self._ca_kv_bits_by_layer.append(sum(1 << kv for kv in by_kv) if foldable else 0)
         self._decode_audio_starts_b = torch.tensor(self._audio_starts_list, dtype=torch.int32, device=self.device)
         self._decode_audio_ends_b = torch.tensor(self._audio_ends_list, dtype=torch.int32, device=self.device)
+        # deferred class-A scoring (slack layout, fused scoring): a foldable
+        # layer's launch keeps its logits in a score slot and the next
+        # launch scores them while its first loads are in flight, so no
+        # scoring launch of its own runs (WNW_DEFER_SCORES=0 turns it off;
+        # a geometry the library does not take turns it off by itself)
+        self._defer_scores = os.environ.get("WNW_DEFER_SCORES", "1") != "0"
+        self._score_slots: list | None = None
+        self._slot_turn = 0
+        # (mask, slot, cu, seg_base, pool_rows, KV-head bits) of a launch not scored yet
+        self._pending_score = None
         # chunk scoring on the device (one launch of wnw_chunk_topk): every
         # sample's chunks as a CSR of token bounds relative to its scores
         B = self.batch_size
@@ -804,6 +816,13 @@ class WnWCache(FlatVarlenCache):
                 and q_flat.shape[1:] == (self.num_q_heads // self.num_kv_heads, self.head_dim)):
             raise _lib.WnwError("q and the new K/V rows must be GPU tensors of the cache's dtype, one per segment")
         app = (nk, nv, self._cu_spare[l], self.seg_cap[l])
+        if fused and self._defer_scores and (score_here or self._pending_score is not None):
+            out = self._deferred_launch(l, q_flat, rows, app, scale, score_here)
+            if out is not None:
+                self._commit_append(l)
+                if not score_here:
+                    self.decode_after_attn(l, q)
+                return out
         if score_here:
             out = q1_decode_attn_score(q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale,
                                        self._ca_kv_mask_by_layer[l], self.num_kv_heads, self._decode_audio_starts_b,
@@ -817,6 +836,47 @@ class WnWCache(FlatVarlenCache):
         if not score_here:
             self.decode_after_attn(l, q)
         return out
+
+    def _deferred_launch(self, l: int, q_flat: Tensor, rows: int, app: tuple, scale: float, score_here: bool):
+        """Layer l's fused append + attention through the deferred-scoring
+        form: its class-A logits kept in a score slot when the layer scores
+        here, the pending slot of an earlier launch scored by this launch.
+        Returns the output, or None (nothing launched, deferral turned off
+        and the pending slot scored in its own launch) where the library does
+        not take the geometry."""
+        N, G = self.batch_size * self.num_kv_heads, self.num_kv_groups
+        if self._score_slots is None:
+            n = score_slot_bytes(N, G, self._max_audio)
+            self._score_slots = [torch.empty((n + 3) // 4, dtype=torch.float32, device=self.device) for _ in range(2)]
+        keep = self._ca_kv_mask_by_layer[l] if score_here else None
+        slot = self._score_slots[self._slot_turn] if score_here else None
+        out = decode_attn_append_deferred(
+            q_flat, self.layer_k[l], self.layer_v[l], self.cu_seqlens_k[l], scale, seg_base=self.seg_base[l],
+            total_rows=rows, append=app, num_kv_heads=self.num_kv_heads, audio_starts=self._decode_audio_starts_b,
+            audio_ends=self._decode_audio_ends_b, max_audio=self._max_audio,
+            score_accumulator=self.score_accumulator, score_offsets=self.score_offsets, keep_mask=keep,
+            keep_slot=slot, prev=self._pending_score)
+        if out is None:
+            self._defer_scores = False
+            self._flush_pending_scores()
+            return None
+        # the segments as this launch saw them: its post-append offsets (the
+        # buffer _commit_append makes current), its pool
+        self._pending_score = (keep, slot, app[2], self.seg_base[l], self.layer_k[l].shape[0],
+                               self._ca_kv_bits_by_layer[l]) if score_here else None
+        if score_here:
+            self._slot_turn ^= 1
+        return out
+
+    def _flush_pending_scores(self) -> None:
+        """Scores the pending slot in a launch of its own (the last foldable
+        layer of a step has no later launch to carry it)."""
+        if self._pending_score is not None:
+            score_kept_logits(self._pending_score, self.batch_size * self.num_kv_heads, self.num_kv_groups,
+                              self.num_kv_heads, self._decode_audio_starts_b, self._decode_audio_ends_b,
+                              self._max_audio, self.score_accumulator, self.score_offsets)
+            self._pending_score = None
+        self._slot_turn = 0
 
     def _commit_append(self, layer_idx: int) -> None:
         """Host bookkeeping of an in-place append: the offsets the append
@@ -870,6 +930,10 @@ class WnWCache(FlatVarlenCache):
             self._rows[l] += n * len(self.seq_lens[l])
         self._decode_step += n
         self._seq_lengths = [x + n for x in self._seq_lengths]
+        # a capture of the fused launches alone leaves its last scored
+        # layer's slot pending; its replays' scores are read by nobody
+        self._pending_score = None
+        self._slot_turn = 0
         if self._planner is not None:
             # the planner counts a plain step when it plans the next one; its
             # lengths are the host's after the last plain step
@@ -996,7 +1060,8 @@ class WnWCache(FlatVarlenCache):
         return out
 
     def decode_all_layers_done(self) -> None:
-        """cache.py:568-576."""
+        """cache.py:568-576 (after the last deferred class-A scores)."""
+        self._flush_pending_scores()
         self._decode_step += 1
         self.stats.flush_decode_step(self._decode_step)
         if self.stats.enabled and self._decode_step % self.stats.interval == 0:

@@ -54,6 +54,7 @@ class WnWCppCache(WnWCache):
         """wnw_cpp/code/cache.py:243-254."""
         if self._fallback:
             return super().decode_all_layers_done()
+        self._flush_pending_scores()  # the step's last deferred class-A scores
         self._decode_step += 1
         self.stats.flush_decode_step(self._decode_step)
         if self.stats.enabled and self._decode_step % self.stats.interval == 0:
