@@ -27,9 +27,10 @@
 // are taken in host-row order, ranges that touch in host memory are merged
 // into spans, and each span is copied by the DMA engines straight from the
 // pinned host rows into the group's rows of a device stage buffer (in that
-// host order); a kernel on the same stream then moves every range from the
-// stage to its transfer-order rows of the outputs, and the group's event is
-// recorded.  With a host layout that keeps a segment's rows of consecutive
+// host order; K spans and V spans on two copy streams of the engine's own);
+// once both are done, a kernel on the job's stream moves every range from
+// the stage to its transfer-order rows of the outputs, and the group's event
+// is recorded.  With a host layout that keeps a segment's rows of consecutive
 // layers together, a group is a few large spans, so the host link is the
 // only bound (the staged form's host memcpy reads and writes every row once
 // more in host memory, which is what kept the DMA engines waiting).
@@ -140,13 +141,15 @@ struct wnw_h2d {
   int64_t* desc_host[2] = {nullptr, nullptr};
   int64_t* desc_dev[2] = {nullptr, nullptr};
   int64_t desc_cap[2] = {0, 0};  // ranges each pair holds
-  // direct form: the V spans go on a second stream (a second DMA engine),
-  // which hides the fixed cost of each copy behind the other stream's
-  // transfers; per parity the job-start event it waits for and per group
-  // the end of its V copies, which the job's stream waits for
-  hipStream_t aux = nullptr;
+  // direct form: the K spans and the V spans go on two streams of their
+  // own (two DMA engines), so each hides the fixed cost of its copies behind
+  // the other's transfers, and neither waits behind a group's permute on the
+  // job's stream; per parity the job-start event both wait for and per group
+  // the ends of their copies, which the job's stream waits for
+  hipStream_t aux_k = nullptr, aux_v = nullptr;
   int aux_device = -1;
   hipEvent_t ev_start[2] = {};
+  hipEvent_t ev_k[2][kMaxGroups] = {};
   hipEvent_t ev_v[2][kMaxGroups] = {};
 };
 
@@ -215,16 +218,19 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
     if (e == hipSuccess) e = hipMalloc((void**)&x->desc_dev[p], (size_t)cap * kDescWords * 8);
     if (e == hipSuccess) x->desc_cap[p] = cap;
   }
-  if (e == hipSuccess && (x->aux == nullptr || x->aux_device != j.device)) {
-    if (x->aux) (void)hipStreamDestroy(x->aux);
-    x->aux = nullptr;
-    e = hipStreamCreateWithFlags(&x->aux, hipStreamNonBlocking);  // default priority
+  if (e == hipSuccess && (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != j.device)) {
+    if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
+    if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
+    x->aux_k = x->aux_v = nullptr;
+    e = hipStreamCreateWithFlags(&x->aux_k, hipStreamNonBlocking);  // default priority
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->aux_v, hipStreamNonBlocking);
     if (e == hipSuccess) x->aux_device = j.device;
   }
-  // the aux stream's copies follow everything queued on the job's stream
-  // before this job (the previous job's permutes read the stage rows)
+  // the copy streams follow everything queued on the job's stream before
+  // this job (the previous job's permutes read the stage rows)
   if (e == hipSuccess) e = hipEventRecord(x->ev_start[p], j.stream);
-  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux, x->ev_start[p], 0);
+  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux_k, x->ev_start[p], 0);
+  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux_v, x->ev_start[p], 0);
   int recorded = 0;
   const int64_t rb = j.row_bytes;
   std::vector<int64_t> ord;
@@ -244,14 +250,15 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
         while (k < ord.size() && j.ranges[2 * ord[k]] == h1) h1 = j.ranges[2 * ord[k++] + 1];
         if (h1 > h0) {
           const size_t bytes = (size_t)((h1 - h0) * rb);
-          e = hipMemcpyAsync(j.stg_k + st0 * rb, j.host_k + h0 * rb, bytes, hipMemcpyHostToDevice, j.stream);
+          e = hipMemcpyAsync(j.stg_k + st0 * rb, j.host_k + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux_k);
           if (e == hipSuccess)
-            e = hipMemcpyAsync(j.stg_v + st0 * rb, j.host_v + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux);
+            e = hipMemcpyAsync(j.stg_v + st0 * rb, j.host_v + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux_v);
         }
         i = k;
       }
-      if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux);
-      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_v[p][g], 0);
+      if (e == hipSuccess) e = hipEventRecord(x->ev_k[p][g], x->aux_k);
+      if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux_v);
+      // the group's permute descriptors go up while its spans are in flight
       int64_t* dh = x->desc_host[p] + a * kDescWords;
       for (int64_t r = a; r < b; ++r) {
         dh[(r - a) * kDescWords] = j.stage_of[r];
@@ -261,6 +268,8 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
       int64_t* dd = x->desc_dev[p] + a * kDescWords;
       if (e == hipSuccess)
         e = hipMemcpyAsync(dd, dh, (size_t)(b - a) * kDescWords * 8, hipMemcpyHostToDevice, j.stream);
+      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_k[p][g], 0);
+      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_v[p][g], 0);
       if (e == hipSuccess) {
         const unsigned grid = (unsigned)std::min<int64_t>(b - a, 1024);
         hipLaunchKernelGGL(stage_permute_kernel, dim3(grid, 2), dim3(256), 0, j.stream,
@@ -328,7 +337,8 @@ void lead_loop(wnw_h2d* x) {
     // so the next job of this parity has nothing to wait for
     if (recorded < x->groups) {
       (void)hipStreamSynchronize(j.stream);
-      if (x->aux) (void)hipStreamSynchronize(x->aux);
+      if (x->aux_k) (void)hipStreamSynchronize(x->aux_k);
+      if (x->aux_v) (void)hipStreamSynchronize(x->aux_v);
       recorded = 0;
     }
     {
@@ -367,8 +377,10 @@ extern "C" wnw_h2d* wnw_h2d_create(int n_workers) {
   bool ok = true;
   for (int p = 0; p < 2; ++p) {
     ok = ok && hipEventCreateWithFlags(&x->ev_start[p], hipEventDisableTiming) == hipSuccess;
-    for (int g = 0; g < kMaxGroups; ++g)
+    for (int g = 0; g < kMaxGroups; ++g) {
+      ok = ok && hipEventCreateWithFlags(&x->ev_k[p][g], hipEventDisableTiming) == hipSuccess;
       ok = ok && hipEventCreateWithFlags(&x->ev_v[p][g], hipEventDisableTiming) == hipSuccess;
+    }
   }
   if (!ok) {
     wnw::set_error("h2d: event creation failed");
@@ -376,6 +388,7 @@ extern "C" wnw_h2d* wnw_h2d_create(int n_workers) {
       if (x->ev_start[p]) (void)hipEventDestroy(x->ev_start[p]);
       for (int g = 0; g < kMaxGroups; ++g) {
         if (x->events[p][g]) (void)hipEventDestroy(x->events[p][g]);
+        if (x->ev_k[p][g]) (void)hipEventDestroy(x->ev_k[p][g]);
         if (x->ev_v[p][g]) (void)hipEventDestroy(x->ev_v[p][g]);
       }
     }
@@ -405,14 +418,19 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
     if (x->last_groups[p] > 0) (void)hipEventSynchronize(x->events[p][x->last_groups[p] - 1]);
   for (int p = 0; p < 2; ++p)
     for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->events[p][g]);
-  if (x->aux) (void)hipStreamSynchronize(x->aux);
+  if (x->aux_k) (void)hipStreamSynchronize(x->aux_k);
+  if (x->aux_v) (void)hipStreamSynchronize(x->aux_v);
   for (int p = 0; p < 2; ++p) {
     if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
     if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
     (void)hipEventDestroy(x->ev_start[p]);
-    for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->ev_v[p][g]);
+    for (int g = 0; g < kMaxGroups; ++g) {
+      (void)hipEventDestroy(x->ev_k[p][g]);
+      (void)hipEventDestroy(x->ev_v[p][g]);
+    }
   }
-  if (x->aux) (void)hipStreamDestroy(x->aux);
+  if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
+  if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
   delete x;
 }
 
