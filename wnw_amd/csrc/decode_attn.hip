@@ -1685,13 +1685,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   wait_vmcnt<0>();
   // deferred scoring, after the stream: every load of the stream is in, so
   // the compiler's wait counts for these loads hold (it does not count the
-  // stream's own loads); the accumulator entry is stored at the very end
-  float* pv_dst = nullptr;
-  float pv_total = 0.f;
-  if constexpr (PV) {
-    prev_issue_body(p, tid, pl);
-    prev_finish(p, tid, pl, pv_dst, pv_total);
-  }
+  // stream's own loads).  They arrive while the waves' states are merged
+  // and the hand-off runs; the sums and the store come at the kernel's end
+  // (summing right after the partials' wait was slower: 26.5 against
+  // 26.3 us per cfg2 layer-step with scoring).
+  if constexpr (PV) prev_issue_body(p, tid, pl);
 
   // ---- shared pieces: merge the waves' states through LDS
   __syncthreads();  // every wave is done with its step buffers (reused below)
@@ -1843,6 +1841,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     }
   }
   wait_vmem();
+  // deferred scoring: its loads are in (the wait above), so its sums cost
+  // no wait here; the accumulator entry is stored at the end
   __syncthreads();  // partials complete; the slots may be overwritten below
   // Both arrivals in one atomic instruction (lanes 0 and 1 of wave 0, one
   // memory round trip); each segment whose last partial this is merges.
@@ -1886,7 +1886,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       if (!lneg && llen + 1 > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
     }
   }
-  if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
+  if constexpr (PV) {
+    float* pv_dst = nullptr;
+    float pv_total = 0.f;
+    prev_finish(p, tid, pl, pv_dst, pv_total);
+    if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
+  }
 }
 
 // ---------------------------------------------------------------------------
