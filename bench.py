@@ -38,6 +38,11 @@ Reported:
 * cpu_baseline  -- the reference's decode layer-step restated in PyTorch
                     (torch.cat append + per-segment float32 attention) on the
                     host's cores, on a bounded sample of the same layers.
+* extras        -- (default cfg2 run only; ``--no-extras`` skips them) child
+                    runs of this script before this process touches the GPU:
+                    cfg2 with class-A scoring (deferred, then the separate
+                    scoring pass) and the cfg4 offload step, so that the
+                    default run reports them too.
 
 ``--copy-calibration`` only runs a plain 256 MiB device-to-device copy three
 times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes).
@@ -47,6 +52,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -72,6 +78,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-compaction", action="store_true", help="skip the compaction and append timings")
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the child runs (scoring, cfg4) that the default cfg2 run adds to its line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy three times (PMC byte calibration)")
     ap.add_argument("--yardstick", action="store_true",
@@ -233,6 +241,9 @@ def main():
 
         print(json.dumps({**offload_bench.run(args.steps, args.warmup), "n_gpus": 1}), flush=True)
         return
+    extras = None
+    if args.config == "cfg2" and not args.score and not args.no_extras:
+        extras = extra_legs()
 
     import numpy as np
     import torch
@@ -400,6 +411,8 @@ def main():
             "kernel": "attn_stream_kernel, fused append + attention", "bytes_per_launch": int(fused_bytes)},
         "cpu_baseline": cpu,
     }
+    if extras is not None:
+        line["extras"] = extras
     rl = line["roofline"]
     ratio = traffic_ratio_from_profiles(cfg.name)
     if rl is not None and ratio is not None:
@@ -414,6 +427,42 @@ def main():
         # the counter-based rate beside the algorithmic one
         rl["traffic_GBs"] = round(rl["traffic"] / (fused_us * 1e-6) / 1e9, 1)
     print(json.dumps(line), flush=True)
+
+
+# child runs of the default cfg2 bench: (key, arguments, environment, fields kept)
+EXTRA_LEGS = [
+    ("score_deferred", ["--score", "--no-cpu", "--no-compaction"], {},
+     ["us_per_layer_step", "ms_per_step", "attn_only_us_per_layer_step"]),
+    ("score_separate_pass", ["--score", "--no-cpu", "--no-compaction"], {"WNW_DEFER_SCORES": "0"},
+     ["us_per_layer_step", "ms_per_step", "attn_only_us_per_layer_step"]),
+    ("offload_cfg4", ["--config", "cfg4"], {},
+     ["value", "unit", "steps", "ms_per_step_staged_path", "ms_per_step_device_path", "ms_per_step_no_offload",
+      "h2d_MB_per_step", "h2d_copy_ms_per_step"]),
+]
+
+
+def extra_legs(timeout_s: int = 600) -> dict:
+    """The extra figures of the default run, each from a child run of this
+    script (one after another, before this process touches the GPU): cfg2
+    with the class-A heads scored every step (deferred scoring, then the
+    separate scoring pass) and the cfg4 offload step.  A leg that fails is
+    reported as such; the headline measurement does not depend on it."""
+    out = {}
+    for key, argv, env, keep in EXTRA_LEGS:
+        cmd = [sys.executable, "-u", os.path.abspath(__file__), "--no-extras", *argv]
+        print(f"# extra leg {key}: {' '.join(argv)} {env or ''}", flush=True)
+        try:
+            r = subprocess.run(cmd, env={**os.environ, **env}, capture_output=True, text=True, timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            out[key] = {"error": f"timed out after {timeout_s} s"}
+            continue
+        lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+        if r.returncode != 0 or not lines:
+            out[key] = {"error": f"exit {r.returncode}: {(r.stderr or r.stdout).strip()[-300:]}"}
+            continue
+        d = json.loads(lines[-1])
+        out[key] = {"args": " ".join(argv), **({"env": env} if env else {}), **{k: d.get(k) for k in keep}}
+    return out
 
 
 def compaction_timing(cfg, cache, inputs, dev, reps: int = 5) -> dict:
