@@ -508,6 +508,15 @@ int wnw_h2d_start_direct(wnw_h2d* x, const void* host_k, const void* host_v,
                          int64_t dev_rows, int64_t row_bytes, void* stream);
 int wnw_h2d_wait(wnw_h2d* x, int group, void* stream);
 int wnw_h2d_join(wnw_h2d* x);
+/*
+ * Set-up costs of the engine paid up front (no reference counterpart: the
+ * reference's channel has none to hide): the copy streams of the direct form
+ * on the current device, descriptor room for n_ranges ranges per job, a
+ * small copy on each stream and an empty job through the engine's thread
+ * on `stream`.  Blocks until done; jobs may follow at once.  Without it the
+ * first jobs pay these costs (tens of ms on MI355X) inside the decode steps.
+ */
+int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Host planner (CPU only; no HIP calls)                                     */

@@ -143,6 +143,48 @@ def test_direct_form_lands_in_transfer_order():
     eng.close()
 
 
+def test_reserve_then_jobs_land_in_transfer_order():
+    """wnw_h2d_reserve (copy streams, descriptor room, an empty job through
+    the engine's thread) before and between direct jobs: room below a job's
+    range count grows on demand, and the rows land as without it."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(21)
+    hk_np, hk = _host_rows(rng, 20000)
+    hv_np, hv = _host_rows(rng, 20000)
+    eng = HostToDevice(workers=2)
+    stream = torch.cuda.Stream(device=dev)
+    eng.reserve(16, stream)  # less room than the jobs below need
+    with torch.cuda.stream(stream):
+        stage = (torch.empty(30000, D, dtype=torch.bfloat16, device=dev),
+                 torch.empty(30000, D, dtype=torch.bfloat16, device=dev))
+    outs = []
+    for job in range(4):
+        if job == 2:
+            eng.reserve(4096, stream)  # between jobs: waits for the engine, then grows both parities
+        ranges, bounds = _case(rng, 20000, int(rng.integers(40, 200)), int(rng.integers(1, 9)))
+        total = int((ranges[:, 1] - ranges[:, 0]).sum())
+        assert total <= 30000
+        with torch.cuda.stream(stream):
+            dk = torch.empty(max(total, 1), D, dtype=torch.bfloat16, device=dev)
+            dv = torch.empty_like(dk)
+        print(f"job {job}: {len(ranges)} ranges, {len(bounds) - 1} groups, {total} rows", flush=True)
+        eng.start_direct(hk, hv, torch.from_numpy(ranges), bounds, stage[0], stage[1], dk, dv, stream)
+        compute = torch.cuda.current_stream(dev)
+        for g in range(len(bounds) - 1):
+            eng.wait(g, compute)
+        outs.append((ranges, dk[:total].clone(), dv[:total].clone()))
+    eng.join()
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    for ranges, got_k, got_v in outs:
+        idx = np.concatenate([np.arange(s, e) for s, e in ranges])
+        np.testing.assert_array_equal(got_k.cpu().view(torch.int16).numpy().view(np.uint16), hk_np[idx])
+        np.testing.assert_array_equal(got_v.cpu().view(torch.int16).numpy().view(np.uint16), hv_np[idx])
+    with pytest.raises(_lib.WnwError):
+        eng.reserve(-1, stream)
+    eng.close()
+
+
 def test_arguments_are_checked():
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(6)

@@ -86,6 +86,7 @@ _SIGNATURES = {
                                     _vp]),
     "wnw_h2d_wait": (_i32, [_vp, _i32, _vp]),
     "wnw_h2d_join": (_i32, [_vp]),
+    "wnw_h2d_reserve": (_i32, [_vp, _i64, _vp]),
 }
 
 

@@ -562,6 +562,65 @@ extern "C" int wnw_h2d_wait(wnw_h2d* x, int group, void* stream) {
   return WNW_OK;
 }
 
+extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream) {
+  using namespace wnw;
+  WNW_CHECK_ARG(x, "h2d: null engine");
+  WNW_CHECK_ARG(n_ranges >= 0 && n_ranges <= (int64_t)1 << 24, "h2d: n_ranges must be in [0, 2^24]");
+  int dev = 0;
+  WNW_CHECK_HIP(hipGetDevice(&dev), "h2d: hipGetDevice");
+  {
+    std::unique_lock<std::mutex> lk(x->mu);
+    join_locked(x, lk);  // the lead thread is idle: its streams and buffers are ours until the next start
+    hipError_t e = hipSuccess;
+    if (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != dev) {
+      if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
+      if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
+      x->aux_k = x->aux_v = nullptr;
+      x->aux_device = -1;
+      e = hipStreamCreateWithFlags(&x->aux_k, hipStreamNonBlocking);  // default priority
+      if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->aux_v, hipStreamNonBlocking);
+      if (e == hipSuccess) x->aux_device = dev;
+    }
+    for (int p = 0; p < 2 && e == hipSuccess; ++p) {
+      if (n_ranges <= x->desc_cap[p] && x->desc_host[p]) continue;
+      // the parity's last copies may still read its descriptors
+      if (x->last_groups[p] > 0) e = hipEventSynchronize(x->events[p][x->last_groups[p] - 1]);
+      if (e != hipSuccess) break;
+      if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
+      if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
+      x->desc_host[p] = nullptr;
+      x->desc_dev[p] = nullptr;
+      x->desc_cap[p] = 0;
+      const int64_t cap = std::max<int64_t>(n_ranges, 1024);
+      e = hipHostMalloc((void**)&x->desc_host[p], (size_t)cap * kDescWords * 8, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipMalloc((void**)&x->desc_dev[p], (size_t)cap * kDescWords * 8);
+      if (e == hipSuccess) {
+        x->desc_cap[p] = cap;
+        memset(x->desc_host[p], 0, 8);
+      }
+    }
+    // one small host-to-device copy on each copy stream, so that their first
+    // real copies find them set up
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(x->desc_dev[0], x->desc_host[0], 8, hipMemcpyHostToDevice, x->aux_k);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(x->desc_dev[1], x->desc_host[1], 8, hipMemcpyHostToDevice, x->aux_v);
+    if (e == hipSuccess) e = hipStreamSynchronize(x->aux_k);
+    if (e == hipSuccess) e = hipStreamSynchronize(x->aux_v);
+    WNW_CHECK_HIP(e, "h2d reserve");
+  }
+  // an empty job through the lead thread (its device, events and the job's
+  // stream set up once)
+  Job j;
+  const int64_t bounds[2] = {0, 0};
+  const int rc = make_job(j, nullptr, nullptr, 0, nullptr, 0, bounds, 1, nullptr, nullptr, 0, nullptr, nullptr, 0, 16,
+                          stream);
+  if (rc != WNW_OK) return rc;
+  j.direct = true;
+  submit(x, std::move(j), 1);
+  return wnw_h2d_join(x);
+}
+
 extern "C" int wnw_h2d_join(wnw_h2d* x) {
   WNW_CHECK_ARG(x, "h2d: null engine");
   std::unique_lock<std::mutex> lk(x->mu);

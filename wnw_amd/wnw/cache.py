@@ -70,7 +70,7 @@ from torch import Tensor
 from .. import _lib
 from ..kv.flat_cache import FlatVarlenCache
 from ..kv.fused_attn import (decode_attn, decode_attn_append_deferred, q1_decode_attn, q1_decode_attn_score,
-                             score_kept_logits, score_slot_bytes)
+                             score_kept_logits, score_slot_bytes, workspace_for)
 from ..kv.kernels import append_inplace, interleave_append_kv
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
@@ -406,6 +406,7 @@ class WnWCache(FlatVarlenCache):
         self._to_slack_layout()
         self._init_planner()
         self._precompute_decode_constants()
+        self._warm_decode_path()
         self.stats.record_prefill(self._snapshot_cache_stats)
 
     def load_prefilled_state(self, layer_k: list[Tensor], layer_v: list[Tensor], seq_lens: list[list[int]],
@@ -428,6 +429,7 @@ class WnWCache(FlatVarlenCache):
         self._to_slack_layout()
         self._init_planner()
         self._precompute_decode_constants()
+        self._warm_decode_path()
 
     def _select_and_apply_chunks(self, b: int, scores: Tensor) -> None:
         """cache.py:603-607: initial chunk choice of a sample, loaded at once."""
@@ -711,9 +713,9 @@ class WnWCache(FlatVarlenCache):
         self._decode_audio_ends_b = torch.tensor(self._audio_ends_list, dtype=torch.int32, device=self.device)
         # deferred class-A scoring (slack layout, fused scoring): a foldable
         # layer's launch keeps its logits in a score slot and the next
-        # launch scores them while its first loads are in flight, so no
-        # scoring launch of its own runs (WNW_DEFER_SCORES=0 turns it off;
-        # a geometry the library does not take turns it off by itself)
+        # launch scores them after its own stream, so no scoring launch of
+        # its own runs except at the step's end (WNW_DEFER_SCORES=0 turns it
+        # off; a geometry the library does not take turns it off by itself)
         self._defer_scores = os.environ.get("WNW_DEFER_SCORES", "1") != "0"
         self._score_slots: list | None = None
         self._slot_turn = 0
@@ -844,10 +846,7 @@ class WnWCache(FlatVarlenCache):
         Returns the output, or None (nothing launched, deferral turned off
         and the pending slot scored in its own launch) where the library does
         not take the geometry."""
-        N, G = self.batch_size * self.num_kv_heads, self.num_kv_groups
-        if self._score_slots is None:
-            n = score_slot_bytes(N, G, self._max_audio)
-            self._score_slots = [torch.empty((n + 3) // 4, dtype=torch.float32, device=self.device) for _ in range(2)]
+        self._ensure_score_slots()
         keep = self._ca_kv_mask_by_layer[l] if score_here else None
         slot = self._score_slots[self._slot_turn] if score_here else None
         out = decode_attn_append_deferred(
@@ -867,6 +866,51 @@ class WnWCache(FlatVarlenCache):
         if score_here:
             self._slot_turn ^= 1
         return out
+
+    def _ensure_score_slots(self) -> None:
+        """The two score slots of deferred scoring (a launch writes one and
+        scores the other)."""
+        if self._score_slots is None:
+            n = score_slot_bytes(self.batch_size * self.num_kv_heads, self.num_kv_groups, self._max_audio)
+            self._score_slots = [torch.empty((n + 3) // 4, dtype=torch.float32, device=self.device) for _ in range(2)]
+
+    def _warm_decode_path(self) -> None:
+        """First-use costs of the decode path paid here, at the end of the
+        prefill, instead of inside the first decode steps (tens of ms on
+        MI355X; cache.py:392-484 warms the reference's Triton kernels for the
+        same reason): the attention workspace of the current stream (with the
+        scoring room when a layer folds its scoring into the attention), the
+        score slots of deferred scoring, one chunk top-k with its copy back,
+        and the transfer engine's copy streams, descriptor room and thread."""
+        N, G, D = self.batch_size * self.num_kv_heads, self.num_kv_groups, self.head_dim
+        ws = workspace_for(self.device)
+        if any(self._layer_foldable):
+            ws.get(N, G, D, score=True, max_audio=self._max_audio)
+            if self._defer_scores and self.slack_layout:
+                self._ensure_score_slots()
+        else:
+            ws.get(N, G, D)
+        if self._tk_k > 0:
+            self._topk_scores_async()
+            self._tk_event.synchronize()
+        if self._offload in ("copy", "staged") and self.cpu_restore_k.shape[0] > 0:
+            if self._h2d is None:
+                self._h2d = HostToDevice()
+            self._h2d.reserve(self._plan_ranges_bound(), self._get_transfer_stream())
+
+    def _plan_ranges_bound(self) -> int:
+        """An upper bound on the host ranges one plan loads: per (layer,
+        sample, class-B head), its offloaded segments, at most
+        ``top_k_chunks`` chunks of the sample's widest chunk."""
+        k = self.config.top_k_chunks
+        total = 0
+        for b in range(self.batch_size):
+            width = max((len(c) for c in self.chunk_to_segs[b]), default=0)
+            for l in range(self.num_layers):
+                for h in range(self.num_kv_heads):
+                    n = sum(1 for m in self.restore_meta[l][b][h] if m is not None)
+                    total += min(n, k * width)
+        return total
 
     def _flush_pending_scores(self) -> None:
         """Scores the pending slot in a launch of its own (the last foldable
