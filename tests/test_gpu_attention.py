@@ -421,13 +421,16 @@ def test_random_configurations(gpu, seed):
 # fused append (wnw_decode_attn_append): the step's row of every segment is
 # written into its slack, and attention covers it
 # ---------------------------------------------------------------------------
-def _append_case(dev, lens, G, D, dtype, seed, shuffle=True, short_cap=None, score=None):
+def _append_case(dev, lens, G, D, dtype, seed, shuffle=True, short_cap=None, score=None, tight=False,
+                 rows_hint=None):
     """Random slack layout (segments in a shuffled physical order with gaps),
-    one fused append + attention; returns what to compare."""
+    one fused append + attention; returns what to compare.  ``tight``: every
+    capacity exactly the length + 1; ``rows_hint``: the row estimate that
+    sizes the grid (default: the rows after the append)."""
     rng = np.random.default_rng(seed)
     n = len(lens)
     lens = np.asarray(lens, np.int64)
-    cap = lens + 1 + rng.integers(0, 6, n)
+    cap = lens + 1 + (0 if tight else rng.integers(0, 6, n))
     if short_cap is not None:
         cap[short_cap] = lens[short_cap]  # no room for the new row
     order = rng.permutation(n) if shuffle else np.arange(n)
@@ -464,7 +467,7 @@ def _append_case(dev, lens, G, D, dtype, seed, shuffle=True, short_cap=None, sco
     tb = torch.from_numpy(base).to(dev)
     if score is None:
         out = fused_attn.decode_attn(to_torch(q, dtype, dev), tk, tv, t32(cu_old), scale, seg_base=tb,
-                                     total_rows=int(cu_new[-1]), append=app)
+                                     total_rows=int(cu_new[-1]) if rows_hint is None else rows_hint, append=app)
         extra = None
     else:
         H, mask, a_s, a_e = score
@@ -510,6 +513,22 @@ def test_fused_append_table_pass(gpu, n_seg):
     rng = np.random.default_rng(n_seg)
     lens = [int(x) for x in rng.integers(0, 900 if n_seg < 1000 else 90, n_seg)]
     _check_append(_append_case(gpu, lens, 4, 128, "bfloat16", seed=n_seg), "bfloat16")
+
+
+def test_fused_append_walks_across_segment_windows(gpu):
+    """A workgroup whose waves walk more than 64 segments (one workgroup, by
+    a small row estimate, over 300 segments): a wave reads its segments in
+    windows of 64, and the walk moves to the next window right after the
+    last step of a window's last segment.  That segment's new row must be
+    kept by its own capacity, not by the next window's: the window-last
+    segments (63, 127, 191, 255) are longer than every segment of the next
+    window, with every capacity exactly the length + 1."""
+    n = 300
+    lens = [2] * n
+    for s, ln in ((63, 40), (127, 30), (191, 20), (255, 10)):
+        lens[s] = ln
+    r = _append_case(gpu, lens, 4, 128, "bfloat16", seed=63, shuffle=True, tight=True, rows_hint=64)
+    _check_append(r, "bfloat16")
 
 
 @pytest.mark.parametrize("case", ["direct", "table_pass"])

@@ -1150,8 +1150,11 @@ struct SStep {
   int32_t s, nrows, seg_len, qslot;
   int32_t first, last, whole;
   int32_t t0, alen;  // audio index of the first row; audio rows whose logits are kept (0: none)
-  int32_t ends_seg;  // APPEND: the step ends its segment (fewer than 16 old rows; the new row is added)
-  int32_t wr;        // APPEND: the segment's lane in the walk's window (its capacity)
+  // APPEND: the step ends its segment (fewer than 16 old rows; the new row
+  // is added): 1, or 2 when the table pass already found that the segment
+  // has no room for the new row in the pool; 0 otherwise
+  int32_t ends_seg;
+  int32_t wr;  // APPEND, direct table: the segment's lane (its capacity is read when the row is kept)
 };
 
 // XL: keep the logits of the scored audio rows (p.xlog), else p.xlog is ignored.
@@ -1380,7 +1383,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     cur_b = (int64_t)(((uint64_t)bhi << 32) | blo);
     cur_lo = __builtin_amdgcn_readlane(llo, k);
     cur_len = __builtin_amdgcn_readlane(llen, k);
-    cur_k = k;  // the segment's lane in the window (its capacity is read when its new row is kept)
+    cur_k = k;  // the segment's lane in the window (its capacity, read by the step that ends it)
     if (XL) {
       cur_a0 = __builtin_amdgcn_readlane(la0, k);
       cur_al = __builtin_amdgcn_readlane(lal, k);
@@ -1407,7 +1410,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       st.t0 = (int32_t)(irow - cur_lo) - cur_a0;
       st.alen = cur_al;
     }
-    st.ends_seg = APPEND && irow + st.nrows == cur_lo + cur_len;
+    // With more than one window of 64 segments (the table pass), the walk
+    // may move on to the next window (next_piece below) before this step is
+    // processed, so the segment's capacity is read now; with the direct
+    // table there is one window, and it is read only when the row is kept.
+    st.ends_seg = 0;
+    if (APPEND && irow + st.nrows == cur_lo + cur_len)
+      st.ends_seg = (!DIRECT && cur_len + 1 > __builtin_amdgcn_readlane(lcap, cur_k)) ? 2 : 1;
     st.wr = cur_k;
     irow += st.nrows;
     st.last = irow >= pe;
@@ -1460,10 +1469,11 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   u32x4 qb[NC];
 
   // APPEND: a segment's new row kept for the pools (stored after the hand-off)
-  // when the segment has room for it; the capacity, loaded with the table,
-  // is read only now.  The row goes after the segment's old rows.
+  // when the segment has room for it.  The row goes after the segment's old
+  // rows.
   auto keep_new_row = [&](const SStep& st) {
-    if (st.seg_len + 1 > __builtin_amdgcn_readlane(lcap, st.wr)) return;  // wave-uniform
+    if (st.ends_seg != 1) return;  // wave-uniform
+    if (DIRECT && st.seg_len + 1 > __builtin_amdgcn_readlane(lcap, st.wr)) return;
     const uint8_t* nrow = qbuf + st.qslot * qslot + qarea;
     const int64_t row = st.row0 + st.nrows;
     if (nsaved < kSaveRows) {  // wave-uniform
