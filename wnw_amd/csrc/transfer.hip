@@ -142,10 +142,11 @@ struct wnw_h2d {
   int64_t* desc_dev[2] = {nullptr, nullptr};
   int64_t desc_cap[2] = {0, 0};  // ranges each pair holds
   // direct form: the K spans and the V spans go on two streams of their
-  // own (two DMA engines), so each hides the fixed cost of its copies behind
-  // the other's transfers, and neither waits behind a group's permute on the
-  // job's stream; per parity the job-start event both wait for and per group
-  // the ends of their copies, which the job's stream waits for
+  // own (two DMA engines; the device's pair, shared by all engines), so each
+  // hides the fixed cost of its copies behind the other's transfers, and
+  // neither waits behind a group's permute on the job's stream; per parity
+  // the job-start event both wait for and per group the ends of their
+  // copies, which the job's stream waits for
   hipStream_t aux_k = nullptr, aux_v = nullptr;
   int aux_device = -1;
   hipEvent_t ev_start[2] = {};
@@ -154,6 +155,28 @@ struct wnw_h2d {
 };
 
 namespace {
+
+// The direct form's two copy streams, one pair per device for the whole
+// process, shared by every engine: HIP maps each new stream onto one of a
+// few hardware queues in turn (GPU_MAX_HW_QUEUES, 4 by default), so streams
+// made per engine (per cache) would in time land on the compute stream's
+// queue, where copies and kernels wait for each other.
+constexpr int kMaxDevices = 64;
+std::mutex g_streams_mu;
+hipStream_t g_copy_k[kMaxDevices] = {}, g_copy_v[kMaxDevices] = {};
+
+hipError_t shared_copy_streams(int dev, hipStream_t* k, hipStream_t* v) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_streams_mu);
+  hipError_t e = hipSuccess;
+  if (!g_copy_k[dev]) e = hipStreamCreateWithFlags(&g_copy_k[dev], hipStreamNonBlocking);  // default priority
+  if (e == hipSuccess && !g_copy_v[dev]) e = hipStreamCreateWithFlags(&g_copy_v[dev], hipStreamNonBlocking);
+  if (e == hipSuccess) {
+    *k = g_copy_k[dev];
+    *v = g_copy_v[dev];
+  }
+  return e;
+}
 
 void copy_ranges(const Job& j, int64_t r0, int64_t r1) {
   for (int64_t r = r0; r < r1; ++r) {
@@ -219,11 +242,7 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
     if (e == hipSuccess) x->desc_cap[p] = cap;
   }
   if (e == hipSuccess && (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != j.device)) {
-    if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
-    if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
-    x->aux_k = x->aux_v = nullptr;
-    e = hipStreamCreateWithFlags(&x->aux_k, hipStreamNonBlocking);  // default priority
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->aux_v, hipStreamNonBlocking);
+    e = shared_copy_streams(j.device, &x->aux_k, &x->aux_v);
     if (e == hipSuccess) x->aux_device = j.device;
   }
   // the copy streams follow everything queued on the job's stream before
@@ -418,8 +437,8 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
     if (x->last_groups[p] > 0) (void)hipEventSynchronize(x->events[p][x->last_groups[p] - 1]);
   for (int p = 0; p < 2; ++p)
     for (int g = 0; g < kMaxGroups; ++g) (void)hipEventDestroy(x->events[p][g]);
-  if (x->aux_k) (void)hipStreamSynchronize(x->aux_k);
-  if (x->aux_v) (void)hipStreamSynchronize(x->aux_v);
+  // (the copy streams are the device's, shared: this engine's copies on them
+  // end before its last events, waited for above)
   for (int p = 0; p < 2; ++p) {
     if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
     if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
@@ -429,8 +448,6 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
       (void)hipEventDestroy(x->ev_v[p][g]);
     }
   }
-  if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
-  if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
   delete x;
 }
 
@@ -573,12 +590,7 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream) {
     join_locked(x, lk);  // the lead thread is idle: its streams and buffers are ours until the next start
     hipError_t e = hipSuccess;
     if (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != dev) {
-      if (x->aux_k) (void)hipStreamDestroy(x->aux_k);
-      if (x->aux_v) (void)hipStreamDestroy(x->aux_v);
-      x->aux_k = x->aux_v = nullptr;
-      x->aux_device = -1;
-      e = hipStreamCreateWithFlags(&x->aux_k, hipStreamNonBlocking);  // default priority
-      if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->aux_v, hipStreamNonBlocking);
+      e = shared_copy_streams(dev, &x->aux_k, &x->aux_v);
       if (e == hipSuccess) x->aux_device = dev;
     }
     for (int p = 0; p < 2 && e == hipSuccess; ++p) {

@@ -75,6 +75,8 @@ from ..kv.kernels import append_inplace, interleave_append_kv
 from ..wnw_cpp.planner import Planner
 from .config import WnWConfig
 from .transfer import HostToDevice
+
+_TRANSFER_STREAMS: dict[int, torch.cuda.Stream] = {}  # device index -> the offload's side stream
 from .kernels import (chunk_topk, compact_segments, fused_score_accumulate, gather_host_rows, host_rows_readable,
                       rebuild_append_kv)
 
@@ -317,8 +319,17 @@ class WnWCache(FlatVarlenCache):
         self._pending_layers_applied = 0
 
     def _get_transfer_stream(self) -> torch.cuda.Stream:
+        """The device's transfer stream, one per device for the process and
+        shared by every cache: HIP maps each new stream onto one of a few
+        hardware queues in turn (GPU_MAX_HW_QUEUES, 4 by default), so a
+        stream made per cache would in time share the compute stream's queue,
+        where the offload's work and the decode kernels wait for each other."""
         if self._transfer_stream is None:
-            self._transfer_stream = torch.cuda.Stream(device=self.device)  # default priority
+            idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
+            st = _TRANSFER_STREAMS.get(idx)
+            if st is None:
+                st = _TRANSFER_STREAMS[idx] = torch.cuda.Stream(device=self.device)  # default priority
+            self._transfer_stream = st
         return self._transfer_stream
 
     # ---------------------------------------------------------------- prefill
