@@ -219,9 +219,9 @@ __device__ __forceinline__ void prev_finish(const AttnParams& p, int tid, const 
   // once per pair and thread
   const float inv_lane = 1.f / pl.l;
   float sum = 0.f, sc = 0.f;
+  int i = 0, g = 0;  // pair t = (flagged KV head i, query head g), uniform, counted (no division by G)
 #pragma unroll
   for (int t = 0; t < kPrevLogits; ++t) {
-    const int i = t / G, g = t - i * G;  // uniform
     if (i < nkv) {
       const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl.m), t));
       const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_lane), t));
@@ -232,6 +232,10 @@ __device__ __forceinline__ void prev_finish(const AttnParams& p, int tid, const 
         sum += sc;
         sc = 0.f;
       }
+    }
+    if (++g == G) {
+      g = 0;
+      ++i;
     }
   }
   if (pl.flags & 1) {
