@@ -169,11 +169,25 @@ __device__ __forceinline__ void prev_issue_body(const AttnParams& p, int tid, Pr
     pl.bv = p.pv_base ? p.pv_base[s] : 0;
   }
   const int64_t jc = min((int64_t)blk * 256 + tid, p.max_audio - 1);
+  // pair t = (flagged KV head i, query head g) reads row (s_i G + g) of the
+  // slot's logits; pairs past the count repeat the last one.  Counted, not
+  // divided: the row offset advances by max_audio per pair (uniform).
+  {
+    const int64_t ma = p.max_audio;
+    const float* xb = p.pv_xlog + jc;
+    int i = 0, g = 0;
+    int64_t cur = (int64_t)(b * Hkv + (int)(p.pv_kvlist & 0xff)) * G * ma, last = cur;
 #pragma unroll
-  for (int t = 0; t < kPrevLogits; ++t) {
-    const int tc = min(t, np - 1), i = tc / G, g = tc - i * G;  // uniform
-    const int s = b * Hkv + (int)((p.pv_kvlist >> (8 * i)) & 0xff);
-    pl.x[t] = p.pv_xlog[((int64_t)s * G + g) * p.max_audio + jc];
+    for (int t = 0; t < kPrevLogits; ++t) {
+      if (t < np) last = cur;
+      pl.x[t] = xb[last];
+      cur += ma;
+      if (++g == G) {
+        g = 0;
+        ++i;
+        cur = (int64_t)(b * Hkv + (int)((p.pv_kvlist >> (8 * min(i, 7))) & 0xff)) * G * ma;
+      }
+    }
   }
   // the entry, clamped into the accumulator (a bad offset is refused later)
   const int off = __builtin_amdgcn_readfirstlane(pl.off);
