@@ -253,19 +253,25 @@ __global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(
   const float prior = p.acc[off + jc];
   const int nt = n_sh * G;
   float total = 0.f, sc = 0.f;  // a segment's heads are summed first, then added to the total
+  // pair t = (segment i, head g), counted rather than divided by G (uniform);
+  // loads past the last pair repeat it
+  int i = 0, g = 0;
   for (int t0 = 0; t0 < nt; t0 += 8) {
     float x[8];
+    int li = i, lg = g;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int t = min(t0 + u, nt - 1);
-      const int i = t / G, g = t - i * G;
-      x[u] = p.xlog[((int64_t)seg_sh[i] * G + g) * p.max_audio + jc];
+      const bool in = t0 + u < nt;
+      const int ii = in ? li : n_sh - 1, gg = in ? lg : G - 1;
+      x[u] = p.xlog[((int64_t)seg_sh[ii] * G + gg) * p.max_audio + jc];
+      if (++lg == G) {
+        lg = 0;
+        ++li;
+      }
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int t = t0 + u;
-      if (t < nt) {
-        const int i = t / G, g = t - i * G;
+      if (t0 + u < nt) {
         // v_exp_f32 directly: arguments are <= 0 (m is the maximum) and
         // weights below 2^-126 (flushed to zero) are negligible
         sc += __builtin_amdgcn_exp2f(x[u] - m_sh[i * kLogitG + g]) * inv_sh[i * kLogitG + g];
@@ -273,6 +279,10 @@ __global__ __launch_bounds__(kLogitThreads) void logit_score_kernel(
           total += sc;
           sc = 0.f;
         }
+      }
+      if (++g == G) {
+        g = 0;
+        ++i;
       }
     }
   }
