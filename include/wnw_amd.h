@@ -66,6 +66,15 @@ int wnw_abi_version(void);
  * points call it lazily otherwise.
  */
 int wnw_init(void);
+/*
+ * Sets up, on the current device, the kernels the decode step launches
+ * outside the attention (scoring pass, chunk top-k, compaction and appends,
+ * the offload channel's kernels): the runtime otherwise does it at each
+ * kernel's first launch, ~1-2 ms each on MI355X, inside the first decode
+ * steps.  No reference counterpart (the reference warms its Triton kernels
+ * instead, src/algorithms/wnw/code/cache.py:392-484).  Always WNW_OK.
+ */
+int wnw_prepare_kernels(void);
 
 /*
  * Reads and optionally clears the device error word of the current device.
@@ -511,12 +520,18 @@ int wnw_h2d_join(wnw_h2d* x);
 /*
  * Set-up costs of the engine paid up front (no reference counterpart: the
  * reference's channel has none to hide): the copy streams of the direct form
- * on the current device, descriptor room for n_ranges ranges per job, a
- * small copy on each stream and an empty job through the engine's thread
- * on `stream`.  Blocks until done; jobs may follow at once.  Without it the
- * first jobs pay these costs (tens of ms on MI355X) inside the decode steps.
+ * on the current device, descriptor room for n_ranges ranges per job, the
+ * DMA engines a job's copies land on (K and V spans issued in turn on the
+ * two copy streams while `stream` copies too: the runtime sets up an
+ * engine's queue at the first copy it puts there, 6-11 ms on MI355X with
+ * every copy submission of the process held meanwhile), the events of the
+ * first n_groups groups (1..64) of both staging parities recorded once, and
+ * an empty job through the engine's thread on `stream` (the stream later
+ * jobs use).  Blocks until done; jobs may follow at once.  Without it the
+ * first jobs pay these costs (tens of ms on MI355X) inside the decode
+ * steps.
  */
-int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream);
+int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Host planner (CPU only; no HIP calls)                                     */

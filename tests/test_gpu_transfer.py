@@ -182,6 +182,8 @@ def test_reserve_then_jobs_land_in_transfer_order():
         np.testing.assert_array_equal(got_v.cpu().view(torch.int16).numpy().view(np.uint16), hv_np[idx])
     with pytest.raises(_lib.WnwError):
         eng.reserve(-1, stream)
+    with pytest.raises(_lib.WnwError):
+        eng.reserve(16, stream, groups=0)
     eng.close()
 
 

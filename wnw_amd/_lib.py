@@ -31,6 +31,7 @@ _SIGNATURES = {
     "wnw_last_error": (ctypes.c_char_p, []),
     "wnw_abi_version": (_i32, []),
     "wnw_init": (_i32, []),
+    "wnw_prepare_kernels": (_i32, []),
     "wnw_device_error": (_i32, [_i32]),
     "wnw_interleave_append": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
     "wnw_interleave_append_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
@@ -86,7 +87,7 @@ _SIGNATURES = {
                                     _vp]),
     "wnw_h2d_wait": (_i32, [_vp, _i32, _vp]),
     "wnw_h2d_join": (_i32, [_vp]),
-    "wnw_h2d_reserve": (_i32, [_vp, _i64, _vp]),
+    "wnw_h2d_reserve": (_i32, [_vp, _i64, _i32, _vp]),
 }
 
 

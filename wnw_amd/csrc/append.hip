@@ -550,3 +550,11 @@ extern "C" int wnw_compact_segments(const void* src_k, const void* src_v, void* 
   WNW_CHECK_HIP(hipGetLastError(), "compact_segments launch");
   return WNW_OK;
 }
+
+void wnw_touch_append_kernels() {
+  hipFuncAttributes a;
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::compact_segments_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::append_inplace_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::rebuild_append_kernel<false>);
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::interleave_append_kernel<true>);
+}

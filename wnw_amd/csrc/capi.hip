@@ -78,6 +78,22 @@ extern "C" int wnw_init(void) {
   return WNW_OK;
 }
 
+// Each source file's kernels of the decode path, resolved on the current
+// device (the runtime sets a kernel up the first time it is used).
+void wnw_touch_score_kernels();
+void wnw_touch_topk_kernels();
+void wnw_touch_transfer_kernels();
+void wnw_touch_append_kernels();
+void wnw_touch_offload_kernels();
+extern "C" int wnw_prepare_kernels(void) {
+  wnw_touch_score_kernels();
+  wnw_touch_topk_kernels();
+  wnw_touch_transfer_kernels();
+  wnw_touch_append_kernels();
+  wnw_touch_offload_kernels();
+  return WNW_OK;
+}
+
 extern "C" int wnw_device_error(int clear) {
   int32_t* w = wnw::device_error_word();
   if (!w) return -1;

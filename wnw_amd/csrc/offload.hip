@@ -113,3 +113,8 @@ extern "C" int wnw_gather_host_rows(const void* host_k, const void* host_v, int6
   WNW_CHECK_HIP(hipGetLastError(), "gather_host_rows launch");
   return WNW_OK;
 }
+
+void wnw_touch_offload_kernels() {
+  hipFuncAttributes a;
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::gather_host_rows_kernel);
+}

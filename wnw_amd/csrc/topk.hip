@@ -241,3 +241,8 @@ extern "C" int wnw_chunk_topk(const float* score_acc, int64_t acc_len, const int
   WNW_CHECK_HIP(hipGetLastError(), "chunk top-k launch");
   return WNW_OK;
 }
+
+void wnw_touch_topk_kernels() {
+  hipFuncAttributes a;
+  (void)hipFuncGetAttributes(&a, (const void*)&wnw::chunk_topk_kernel);
+}

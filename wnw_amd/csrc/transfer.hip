@@ -579,10 +579,11 @@ extern "C" int wnw_h2d_wait(wnw_h2d* x, int group, void* stream) {
   return WNW_OK;
 }
 
-extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream) {
+extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void* stream) {
   using namespace wnw;
   WNW_CHECK_ARG(x, "h2d: null engine");
   WNW_CHECK_ARG(n_ranges >= 0 && n_ranges <= (int64_t)1 << 24, "h2d: n_ranges must be in [0, 2^24]");
+  WNW_CHECK_ARG(n_groups >= 1 && n_groups <= kMaxGroups, "h2d: n_groups must be in [1, %d]", kMaxGroups);
   int dev = 0;
   WNW_CHECK_HIP(hipGetDevice(&dev), "h2d: hipGetDevice");
   {
@@ -606,19 +607,55 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, void* stream) {
       const int64_t cap = std::max<int64_t>(n_ranges, 1024);
       e = hipHostMalloc((void**)&x->desc_host[p], (size_t)cap * kDescWords * 8, hipHostMallocDefault);
       if (e == hipSuccess) e = hipMalloc((void**)&x->desc_dev[p], (size_t)cap * kDescWords * 8);
-      if (e == hipSuccess) {
-        x->desc_cap[p] = cap;
-        memset(x->desc_host[p], 0, 8);
+      if (e == hipSuccess) x->desc_cap[p] = cap;
+    }
+    // The copy engines: the runtime puts a stream's copy on another DMA
+    // engine when the one it used last is busy, and sets up an engine's
+    // queue the first time a copy lands on it (6-11 ms on MI355X, every copy
+    // submission of the process held meanwhile).  Spans of K and V issued in
+    // turn on the two copy streams while the job's stream copies too, as in
+    // a job, twice (the two parities' first jobs met a new engine each
+    // otherwise), so that the engines a job's copies land on are set up here.
+    const hipStream_t js = (hipStream_t)stream;
+    {
+      constexpr size_t kSpan = 512u << 10;
+      constexpr int kSpans = 24;
+      const size_t total = (2 * kSpans + 4) * kSpan;
+      char* hb = nullptr;
+      char* db = nullptr;
+      if (e == hipSuccess) e = hipHostMalloc((void**)&hb, total, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipMalloc((void**)&db, total);
+      if (e == hipSuccess) memset(hb, 0, total);
+      for (int rep = 0; rep < 2 && e == hipSuccess; ++rep) {
+        for (int i = 0; i < kSpans && e == hipSuccess; ++i) {
+          const size_t o = (size_t)(2 * i) * kSpan;
+          e = hipMemcpyAsync(db + o, hb + o, kSpan, hipMemcpyHostToDevice, x->aux_k);
+          if (e == hipSuccess) e = hipMemcpyAsync(db + o + kSpan, hb + o + kSpan, kSpan, hipMemcpyHostToDevice, x->aux_v);
+          if (e == hipSuccess && i % 8 == 4) {
+            const size_t q = (size_t)(2 * kSpans + i / 8) * kSpan;
+            e = hipMemcpyAsync(db + q, hb + q, kSpan, hipMemcpyHostToDevice, js);
+          }
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(x->aux_k);
+        if (e == hipSuccess) e = hipStreamSynchronize(x->aux_v);
+        if (e == hipSuccess) e = hipStreamSynchronize(js);
+      }
+      if (db) (void)hipFree(db);
+      if (hb) (void)hipHostFree(hb);
+    }
+    // every event of the first n_groups groups recorded once, on the stream
+    // a job records it on
+    for (int p = 0; p < 2 && e == hipSuccess; ++p) {
+      e = hipEventRecord(x->ev_start[p], js);
+      for (int g = 0; g < n_groups && e == hipSuccess; ++g) {
+        e = hipEventRecord(x->ev_k[p][g], x->aux_k);
+        if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux_v);
+        if (e == hipSuccess) e = hipEventRecord(x->events[p][g], js);
       }
     }
-    // one small host-to-device copy on each copy stream, so that their first
-    // real copies find them set up
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(x->desc_dev[0], x->desc_host[0], 8, hipMemcpyHostToDevice, x->aux_k);
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(x->desc_dev[1], x->desc_host[1], 8, hipMemcpyHostToDevice, x->aux_v);
     if (e == hipSuccess) e = hipStreamSynchronize(x->aux_k);
     if (e == hipSuccess) e = hipStreamSynchronize(x->aux_v);
+    if (e == hipSuccess) e = hipStreamSynchronize(js);
     WNW_CHECK_HIP(e, "h2d reserve");
   }
   // an empty job through the lead thread (its device, events and the job's
@@ -639,4 +676,9 @@ extern "C" int wnw_h2d_join(wnw_h2d* x) {
   join_locked(x, lk);
   if (x->error != WNW_OK) wnw::set_error("%s", x->error_msg);
   return x->error;
+}
+
+void wnw_touch_transfer_kernels() {
+  hipFuncAttributes a;
+  (void)hipFuncGetAttributes(&a, (const void*)&stage_permute_kernel);
 }

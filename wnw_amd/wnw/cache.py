@@ -892,8 +892,12 @@ class WnWCache(FlatVarlenCache):
         same reason): the attention workspace of the current stream (with the
         scoring room when a layer folds its scoring into the attention), the
         score slots of deferred scoring, one chunk top-k with its copy back,
-        and the transfer engine's copy streams, descriptor room and thread."""
+        and the transfer engine's copy streams, DMA engines, events,
+        descriptor room and thread; and the kernels launched outside the
+        attention, set up on the device (``wnw_prepare_kernels``)."""
         N, G, D = self.batch_size * self.num_kv_heads, self.num_kv_groups, self.head_dim
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().wnw_prepare_kernels(), "wnw_prepare_kernels")
         ws = workspace_for(self.device)
         if any(self._layer_foldable):
             ws.get(N, G, D, score=True, max_audio=self._max_audio)
@@ -907,7 +911,7 @@ class WnWCache(FlatVarlenCache):
         if self._offload in ("copy", "staged") and self.cpu_restore_k.shape[0] > 0:
             if self._h2d is None:
                 self._h2d = HostToDevice()
-            self._h2d.reserve(self._plan_ranges_bound(), self._get_transfer_stream())
+            self._h2d.reserve(self._plan_ranges_bound(), self._get_transfer_stream(), len(self._group_layers()))
 
     def _plan_ranges_bound(self) -> int:
         """An upper bound on the host ranges one plan loads: per (layer,

@@ -102,13 +102,15 @@ class HostToDevice:
             len(group_ranges) - 1, _lib.ptr(stage_k), _lib.ptr(stage_v), stage_k.shape[0], _lib.ptr(dev_k),
             _lib.ptr(dev_v), dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream)), "h2d start_direct")
 
-    def reserve(self, n_ranges: int, stream: torch.cuda.Stream) -> None:
+    def reserve(self, n_ranges: int, stream: torch.cuda.Stream, groups: int = 8) -> None:
         """Pays the engine's set-up costs now (``wnw_h2d_reserve``): the
         direct form's copy streams on the current device, descriptor room for
-        ``n_ranges`` ranges per job, and an empty job through the engine's
-        thread on ``stream``.  Blocks until done."""
-        _lib.check(_lib.lib().wnw_h2d_reserve(self._h, int(n_ranges), ctypes.c_void_p(stream.cuda_stream)),
-                   "h2d reserve")
+        ``n_ranges`` ranges per job, the DMA engines a job's copies land on
+        (a job's copy pattern replayed on scratch buffers), the events of the
+        first ``groups`` groups, and an empty job through the engine's thread
+        on ``stream``.  Blocks until done."""
+        _lib.check(_lib.lib().wnw_h2d_reserve(self._h, int(n_ranges), int(groups),
+                                              ctypes.c_void_p(stream.cuda_stream)), "h2d reserve")
 
     def wait(self, group: int, stream: torch.cuda.Stream | None = None) -> None:
         """``stream`` (default: the current one) waits for group ``group``'s
