@@ -52,7 +52,6 @@
 namespace wnw {
 
 static constexpr int kMaxGroup = 16;
-static constexpr int kMaxGroupPrev = 8;  // query heads per KV head of the deferred scoring (the streaming kernel's limit)
 static constexpr int kRing = 64;  // LDS cache of segment bounds per workgroup
 static constexpr float kNegBig = -1e30f;
 static constexpr float kLog2e = 1.4426950408889634f;

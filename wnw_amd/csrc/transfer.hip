@@ -27,7 +27,8 @@
 // are taken in host-row order, ranges that touch in host memory are merged
 // into spans, and each span is copied by the DMA engines straight from the
 // pinned host rows into the group's rows of a device stage buffer (in that
-// host order; K spans and V spans on two copy streams of the engine's own);
+// host order; the spans' K and V copies dealt in turn over two copy
+// streams, the device's pair);
 // once both are done, a kernel on the job's stream moves every range from
 // the stage to its transfer-order rows of the outputs, and the group's event
 // is recorded.  With a host layout that keeps a segment's rows of consecutive
@@ -37,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <condition_variable>
 #include <cstdio>
 #include <cstring>
@@ -50,6 +52,13 @@
 namespace {
 
 constexpr int kMaxGroups = 64;
+// copy streams of the direct form: the spans' copies are dealt over them in
+// turn.  On MI355X, 130 copies of ~1.2 MB from pinned rows ran at 39.8 GB/s
+// on one stream, 51.5 on two, 55.2 on four and 52.8 on eight.  Four made a
+// cfg4 step only ~1.5 % faster (3.34 against 3.38-3.40 ms) and moved the
+// compute stream's own small copies onto new DMA engines during the first
+// steps (7-10 ms set-ups that no warm-up of these streams removed): two.
+constexpr int kCopyStreams = 2;
 
 struct Job {
   const char* host_k = nullptr;
@@ -141,40 +150,53 @@ struct wnw_h2d {
   int64_t* desc_host[2] = {nullptr, nullptr};
   int64_t* desc_dev[2] = {nullptr, nullptr};
   int64_t desc_cap[2] = {0, 0};  // ranges each pair holds
-  // direct form: the K spans and the V spans go on two streams of their
-  // own (two DMA engines; the device's pair, shared by all engines), so each
-  // hides the fixed cost of its copies behind the other's transfers, and
-  // neither waits behind a group's permute on the job's stream; per parity
-  // the job-start event both wait for and per group the ends of their
-  // copies, which the job's stream waits for
-  hipStream_t aux_k = nullptr, aux_v = nullptr;
+  // direct form: the spans' K and V copies are dealt in turn over
+  // kCopyStreams streams of their own (DMA engines; the device's set, shared
+  // by all engines), so each hides the fixed cost of its copies behind the
+  // others' transfers, and none waits behind a group's permute on the job's
+  // stream; per parity the job-start event they all wait for and per group
+  // the ends of their copies, which the job's stream waits for (created at
+  // first use)
+  hipStream_t aux[kCopyStreams] = {};
   int aux_device = -1;
   hipEvent_t ev_start[2] = {};
-  hipEvent_t ev_k[2][kMaxGroups] = {};
-  hipEvent_t ev_v[2][kMaxGroups] = {};
+  hipEvent_t ev_copy[2][kMaxGroups][kCopyStreams] = {};
 };
 
 namespace {
 
-// The direct form's two copy streams, one pair per device for the whole
+// The direct form's copy streams, one set per device for the whole
 // process, shared by every engine: HIP maps each new stream onto one of a
 // few hardware queues in turn (GPU_MAX_HW_QUEUES, 4 by default), so streams
 // made per engine (per cache) would in time land on the compute stream's
 // queue, where copies and kernels wait for each other.
 constexpr int kMaxDevices = 64;
 std::mutex g_streams_mu;
-hipStream_t g_copy_k[kMaxDevices] = {}, g_copy_v[kMaxDevices] = {};
+hipStream_t g_copy[kMaxDevices][kCopyStreams] = {};
 
-hipError_t shared_copy_streams(int dev, hipStream_t* k, hipStream_t* v) {
+hipError_t shared_copy_streams(int dev, hipStream_t* out) {
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(g_streams_mu);
   hipError_t e = hipSuccess;
-  if (!g_copy_k[dev]) e = hipStreamCreateWithFlags(&g_copy_k[dev], hipStreamNonBlocking);  // default priority
-  if (e == hipSuccess && !g_copy_v[dev]) e = hipStreamCreateWithFlags(&g_copy_v[dev], hipStreamNonBlocking);
-  if (e == hipSuccess) {
-    *k = g_copy_k[dev];
-    *v = g_copy_v[dev];
+  for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c)
+    if (!g_copy[dev][c]) e = hipStreamCreateWithFlags(&g_copy[dev][c], hipStreamNonBlocking);  // default priority
+  if (e == hipSuccess)
+    for (int c = 0; c < kCopyStreams; ++c) out[c] = g_copy[dev][c];
+  return e;
+}
+
+// The engine's copy streams on `dev` (set up once per device) and the copy
+// events of its first n_groups groups (created once).
+hipError_t direct_setup(wnw_h2d* x, int dev, int n_groups) {
+  hipError_t e = hipSuccess;
+  if (x->aux[0] == nullptr || x->aux_device != dev) {
+    e = shared_copy_streams(dev, x->aux);
+    if (e == hipSuccess) x->aux_device = dev;
   }
+  for (int p = 0; p < 2 && e == hipSuccess; ++p)
+    for (int g = 0; g < n_groups && e == hipSuccess; ++g)
+      for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c)
+        if (!x->ev_copy[p][g][c]) e = hipEventCreateWithFlags(&x->ev_copy[p][g][c], hipEventDisableTiming);
   return e;
 }
 
@@ -241,18 +263,15 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
     if (e == hipSuccess) e = hipMalloc((void**)&x->desc_dev[p], (size_t)cap * kDescWords * 8);
     if (e == hipSuccess) x->desc_cap[p] = cap;
   }
-  if (e == hipSuccess && (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != j.device)) {
-    e = shared_copy_streams(j.device, &x->aux_k, &x->aux_v);
-    if (e == hipSuccess) x->aux_device = j.device;
-  }
+  if (e == hipSuccess) e = direct_setup(x, j.device, x->groups);
   // the copy streams follow everything queued on the job's stream before
   // this job (the previous job's permutes read the stage rows)
   if (e == hipSuccess) e = hipEventRecord(x->ev_start[p], j.stream);
-  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux_k, x->ev_start[p], 0);
-  if (e == hipSuccess) e = hipStreamWaitEvent(x->aux_v, x->ev_start[p], 0);
+  for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) e = hipStreamWaitEvent(x->aux[c], x->ev_start[p], 0);
   int recorded = 0;
   const int64_t rb = j.row_bytes;
   std::vector<int64_t> ord;
+  int next = 0;  // the copy stream of the next copy (dealt in turn over the job)
   for (int g = 0; g < x->groups; ++g) {
     const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
     if (e == hipSuccess && b > a) {
@@ -261,6 +280,7 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
       ord.resize(b - a);
       for (int64_t r = a; r < b; ++r) ord[r - a] = r;
       std::sort(ord.begin(), ord.end(), [&](int64_t u, int64_t v) { return j.stage_of[u] < j.stage_of[v]; });
+      bool used[kCopyStreams] = {};
       for (size_t i = 0; i < ord.size() && e == hipSuccess;) {
         const int64_t r0 = ord[i];
         const int64_t h0 = j.ranges[2 * r0], st0 = j.stage_of[r0];
@@ -269,14 +289,20 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
         while (k < ord.size() && j.ranges[2 * ord[k]] == h1) h1 = j.ranges[2 * ord[k++] + 1];
         if (h1 > h0) {
           const size_t bytes = (size_t)((h1 - h0) * rb);
-          e = hipMemcpyAsync(j.stg_k + st0 * rb, j.host_k + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux_k);
+          e = hipMemcpyAsync(j.stg_k + st0 * rb, j.host_k + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux[next]);
+          used[next] = true;
+          next = (next + 1) % kCopyStreams;
           if (e == hipSuccess)
-            e = hipMemcpyAsync(j.stg_v + st0 * rb, j.host_v + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux_v);
+            e = hipMemcpyAsync(j.stg_v + st0 * rb, j.host_v + h0 * rb, bytes, hipMemcpyHostToDevice, x->aux[next]);
+          used[next] = true;
+          next = (next + 1) % kCopyStreams;
         }
         i = k;
       }
-      if (e == hipSuccess) e = hipEventRecord(x->ev_k[p][g], x->aux_k);
-      if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux_v);
+      // the end of the group's copies on each stream that took some (the
+      // job's stream has waited for every earlier copy on the others)
+      for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c)
+        if (used[c]) e = hipEventRecord(x->ev_copy[p][g][c], x->aux[c]);
       // the group's permute descriptors go up while its spans are in flight
       int64_t* dh = x->desc_host[p] + a * kDescWords;
       for (int64_t r = a; r < b; ++r) {
@@ -287,8 +313,8 @@ int run_direct(wnw_h2d* x, const Job& j, hipError_t e) {
       int64_t* dd = x->desc_dev[p] + a * kDescWords;
       if (e == hipSuccess)
         e = hipMemcpyAsync(dd, dh, (size_t)(b - a) * kDescWords * 8, hipMemcpyHostToDevice, j.stream);
-      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_k[p][g], 0);
-      if (e == hipSuccess) e = hipStreamWaitEvent(j.stream, x->ev_v[p][g], 0);
+      for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c)
+        if (used[c]) e = hipStreamWaitEvent(j.stream, x->ev_copy[p][g][c], 0);
       if (e == hipSuccess) {
         const unsigned grid = (unsigned)std::min<int64_t>(b - a, 1024);
         hipLaunchKernelGGL(stage_permute_kernel, dim3(grid, 2), dim3(256), 0, j.stream,
@@ -356,8 +382,8 @@ void lead_loop(wnw_h2d* x) {
     // so the next job of this parity has nothing to wait for
     if (recorded < x->groups) {
       (void)hipStreamSynchronize(j.stream);
-      if (x->aux_k) (void)hipStreamSynchronize(x->aux_k);
-      if (x->aux_v) (void)hipStreamSynchronize(x->aux_v);
+      for (int c = 0; c < kCopyStreams; ++c)
+        if (x->aux[c]) (void)hipStreamSynchronize(x->aux[c]);
       recorded = 0;
     }
     {
@@ -394,22 +420,14 @@ extern "C" wnw_h2d* wnw_h2d_create(int n_workers) {
       }
     }
   bool ok = true;
-  for (int p = 0; p < 2; ++p) {
+  for (int p = 0; p < 2; ++p)
     ok = ok && hipEventCreateWithFlags(&x->ev_start[p], hipEventDisableTiming) == hipSuccess;
-    for (int g = 0; g < kMaxGroups; ++g) {
-      ok = ok && hipEventCreateWithFlags(&x->ev_k[p][g], hipEventDisableTiming) == hipSuccess;
-      ok = ok && hipEventCreateWithFlags(&x->ev_v[p][g], hipEventDisableTiming) == hipSuccess;
-    }
-  }
   if (!ok) {
     wnw::set_error("h2d: event creation failed");
     for (int p = 0; p < 2; ++p) {
       if (x->ev_start[p]) (void)hipEventDestroy(x->ev_start[p]);
-      for (int g = 0; g < kMaxGroups; ++g) {
+      for (int g = 0; g < kMaxGroups; ++g)
         if (x->events[p][g]) (void)hipEventDestroy(x->events[p][g]);
-        if (x->ev_k[p][g]) (void)hipEventDestroy(x->ev_k[p][g]);
-        if (x->ev_v[p][g]) (void)hipEventDestroy(x->ev_v[p][g]);
-      }
     }
     delete x;
     return nullptr;
@@ -443,10 +461,9 @@ extern "C" void wnw_h2d_destroy(wnw_h2d* x) {
     if (x->desc_host[p]) (void)hipHostFree(x->desc_host[p]);
     if (x->desc_dev[p]) (void)hipFree(x->desc_dev[p]);
     (void)hipEventDestroy(x->ev_start[p]);
-    for (int g = 0; g < kMaxGroups; ++g) {
-      (void)hipEventDestroy(x->ev_k[p][g]);
-      (void)hipEventDestroy(x->ev_v[p][g]);
-    }
+    for (int g = 0; g < kMaxGroups; ++g)
+      for (int c = 0; c < kCopyStreams; ++c)
+        if (x->ev_copy[p][g][c]) (void)hipEventDestroy(x->ev_copy[p][g][c]);
   }
   delete x;
 }
@@ -590,10 +607,7 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void*
     std::unique_lock<std::mutex> lk(x->mu);
     join_locked(x, lk);  // the lead thread is idle: its streams and buffers are ours until the next start
     hipError_t e = hipSuccess;
-    if (x->aux_k == nullptr || x->aux_v == nullptr || x->aux_device != dev) {
-      e = shared_copy_streams(dev, &x->aux_k, &x->aux_v);
-      if (e == hipSuccess) x->aux_device = dev;
-    }
+    e = direct_setup(x, dev, n_groups);
     for (int p = 0; p < 2 && e == hipSuccess; ++p) {
       if (n_ranges <= x->desc_cap[p] && x->desc_host[p]) continue;
       // the parity's last copies may still read its descriptors
@@ -612,33 +626,38 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void*
     // The copy engines: the runtime puts a stream's copy on another DMA
     // engine when the one it used last is busy, and sets up an engine's
     // queue the first time a copy lands on it (6-11 ms on MI355X, every copy
-    // submission of the process held meanwhile).  Spans of K and V issued in
-    // turn on the two copy streams while the job's stream copies too, as in
-    // a job, twice (the two parities' first jobs met a new engine each
-    // otherwise), so that the engines a job's copies land on are set up here.
+    // submission of the process held meanwhile; a job's first copies met
+    // one or two such set-ups otherwise).  Spans of a job's sizes are issued
+    // in turn on the copy streams while the job's stream copies too, round
+    // after round until a whole round has no submission slower than 1 ms
+    // (at most kWarmRounds), so that the engines a job's copies land on are
+    // set up here.
     const hipStream_t js = (hipStream_t)stream;
     {
-      constexpr size_t kSpan = 512u << 10;
-      constexpr int kSpans = 24;
-      const size_t total = (2 * kSpans + 4) * kSpan;
+      constexpr size_t kBuf = 8u << 20;
+      constexpr int kCopies = 64;
+      constexpr int kWarmRounds = 12;
+      constexpr size_t kSizes[4] = {384u << 10, 1536u << 10, 768u << 10, 2560u << 10};
       char* hb = nullptr;
       char* db = nullptr;
-      if (e == hipSuccess) e = hipHostMalloc((void**)&hb, total, hipHostMallocDefault);
-      if (e == hipSuccess) e = hipMalloc((void**)&db, total);
-      if (e == hipSuccess) memset(hb, 0, total);
-      for (int rep = 0; rep < 2 && e == hipSuccess; ++rep) {
-        for (int i = 0; i < kSpans && e == hipSuccess; ++i) {
-          const size_t o = (size_t)(2 * i) * kSpan;
-          e = hipMemcpyAsync(db + o, hb + o, kSpan, hipMemcpyHostToDevice, x->aux_k);
-          if (e == hipSuccess) e = hipMemcpyAsync(db + o + kSpan, hb + o + kSpan, kSpan, hipMemcpyHostToDevice, x->aux_v);
-          if (e == hipSuccess && i % 8 == 4) {
-            const size_t q = (size_t)(2 * kSpans + i / 8) * kSpan;
-            e = hipMemcpyAsync(db + q, hb + q, kSpan, hipMemcpyHostToDevice, js);
-          }
+      if (e == hipSuccess) e = hipHostMalloc((void**)&hb, kBuf, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipMalloc((void**)&db, kBuf);
+      if (e == hipSuccess) memset(hb, 0, kBuf);
+      for (int round = 0; round < kWarmRounds && e == hipSuccess; ++round) {
+        double slowest = 0.0;
+        size_t o = 0;
+        for (int i = 0; i < kCopies && e == hipSuccess; ++i) {
+          const size_t n = kSizes[(i + round) % 4];
+          if (o + n > kBuf) o = 0;
+          const auto t0 = std::chrono::steady_clock::now();
+          e = hipMemcpyAsync(db + o, hb + o, n, hipMemcpyHostToDevice, x->aux[i % kCopyStreams]);
+          if (e == hipSuccess && i % 16 == 8) e = hipMemcpyAsync(db, hb, 64u << 10, hipMemcpyHostToDevice, js);
+          slowest = std::max(slowest, std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+          o += n;
         }
-        if (e == hipSuccess) e = hipStreamSynchronize(x->aux_k);
-        if (e == hipSuccess) e = hipStreamSynchronize(x->aux_v);
+        for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) e = hipStreamSynchronize(x->aux[c]);
         if (e == hipSuccess) e = hipStreamSynchronize(js);
+        if (round >= 1 && slowest < 1e-3) break;
       }
       if (db) (void)hipFree(db);
       if (hb) (void)hipHostFree(hb);
@@ -648,13 +667,11 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void*
     for (int p = 0; p < 2 && e == hipSuccess; ++p) {
       e = hipEventRecord(x->ev_start[p], js);
       for (int g = 0; g < n_groups && e == hipSuccess; ++g) {
-        e = hipEventRecord(x->ev_k[p][g], x->aux_k);
-        if (e == hipSuccess) e = hipEventRecord(x->ev_v[p][g], x->aux_v);
+        for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) e = hipEventRecord(x->ev_copy[p][g][c], x->aux[c]);
         if (e == hipSuccess) e = hipEventRecord(x->events[p][g], js);
       }
     }
-    if (e == hipSuccess) e = hipStreamSynchronize(x->aux_k);
-    if (e == hipSuccess) e = hipStreamSynchronize(x->aux_v);
+    for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) e = hipStreamSynchronize(x->aux[c]);
     if (e == hipSuccess) e = hipStreamSynchronize(js);
     WNW_CHECK_HIP(e, "h2d reserve");
   }
