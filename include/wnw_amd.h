@@ -521,9 +521,8 @@ int wnw_h2d_join(wnw_h2d* x);
  * Set-up costs of the engine paid up front (no reference counterpart: the
  * reference's channel has none to hide): the copy streams of the direct form
  * on the current device, descriptor room for n_ranges ranges per job, the
- * DMA engines a job's copies land on (spans of a job's sizes issued in turn
- * on the copy streams while `stream` copies too, round after round until a
- * round has no submission slower than 1 ms: the runtime sets up an
+ * DMA engines a job's copies land on (spans issued in turn on the copy
+ * streams while `stream` copies too, twice: the runtime sets up an
  * engine's queue at the first copy it puts there, 6-11 ms on MI355X with
  * every copy submission of the process held meanwhile), the events of the
  * first n_groups groups (1..64) of both staging parities recorded once, and

@@ -38,7 +38,6 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <chrono>
 #include <condition_variable>
 #include <cstdio>
 #include <cstring>
@@ -626,38 +625,33 @@ extern "C" int wnw_h2d_reserve(wnw_h2d* x, int64_t n_ranges, int n_groups, void*
     // The copy engines: the runtime puts a stream's copy on another DMA
     // engine when the one it used last is busy, and sets up an engine's
     // queue the first time a copy lands on it (6-11 ms on MI355X, every copy
-    // submission of the process held meanwhile; a job's first copies met
-    // one or two such set-ups otherwise).  Spans of a job's sizes are issued
-    // in turn on the copy streams while the job's stream copies too, round
-    // after round until a whole round has no submission slower than 1 ms
-    // (at most kWarmRounds), so that the engines a job's copies land on are
-    // set up here.
+    // submission of the process held meanwhile; the first job of each
+    // staging parity met one otherwise).  Spans issued in turn on the copy
+    // streams while the job's stream copies too, as in a job, twice, so that
+    // the engines a job's copies land on are set up here.  (Repeating rounds
+    // of mixed span sizes until no submission took over 1 ms left the
+    // streams on engines that ran cfg4 steps ~0.08 ms slower.)
     const hipStream_t js = (hipStream_t)stream;
     {
-      constexpr size_t kBuf = 8u << 20;
-      constexpr int kCopies = 64;
-      constexpr int kWarmRounds = 12;
-      constexpr size_t kSizes[4] = {384u << 10, 1536u << 10, 768u << 10, 2560u << 10};
+      constexpr size_t kSpan = 512u << 10;
+      constexpr int kCopies = 48;
+      const size_t total = (kCopies + 4) * kSpan;
       char* hb = nullptr;
       char* db = nullptr;
-      if (e == hipSuccess) e = hipHostMalloc((void**)&hb, kBuf, hipHostMallocDefault);
-      if (e == hipSuccess) e = hipMalloc((void**)&db, kBuf);
-      if (e == hipSuccess) memset(hb, 0, kBuf);
-      for (int round = 0; round < kWarmRounds && e == hipSuccess; ++round) {
-        double slowest = 0.0;
-        size_t o = 0;
+      if (e == hipSuccess) e = hipHostMalloc((void**)&hb, total, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipMalloc((void**)&db, total);
+      if (e == hipSuccess) memset(hb, 0, total);
+      for (int round = 0; round < 2 && e == hipSuccess; ++round) {
         for (int i = 0; i < kCopies && e == hipSuccess; ++i) {
-          const size_t n = kSizes[(i + round) % 4];
-          if (o + n > kBuf) o = 0;
-          const auto t0 = std::chrono::steady_clock::now();
-          e = hipMemcpyAsync(db + o, hb + o, n, hipMemcpyHostToDevice, x->aux[i % kCopyStreams]);
-          if (e == hipSuccess && i % 16 == 8) e = hipMemcpyAsync(db, hb, 64u << 10, hipMemcpyHostToDevice, js);
-          slowest = std::max(slowest, std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
-          o += n;
+          const size_t o = (size_t)i * kSpan;
+          e = hipMemcpyAsync(db + o, hb + o, kSpan, hipMemcpyHostToDevice, x->aux[i % kCopyStreams]);
+          if (e == hipSuccess && i % 16 == 9) {
+            const size_t q = (size_t)(kCopies + i / 16) * kSpan;
+            e = hipMemcpyAsync(db + q, hb + q, kSpan, hipMemcpyHostToDevice, js);
+          }
         }
         for (int c = 0; c < kCopyStreams && e == hipSuccess; ++c) e = hipStreamSynchronize(x->aux[c]);
         if (e == hipSuccess) e = hipStreamSynchronize(js);
-        if (round >= 1 && slowest < 1e-3) break;
       }
       if (db) (void)hipFree(db);
       if (hb) (void)hipHostFree(hb);
