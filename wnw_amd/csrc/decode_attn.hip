@@ -108,20 +108,18 @@ struct AttnParams {
   int32_t pv_slices;  // samples x pv_nblk (<= the grid)
 };
 
-// Deferred scoring of the previous launch's kept logits.  Workgroup i < the
-// slice count takes slice i = (sample b, block of 256 audio tokens), one
-// token per thread; the other workgroups load slice 0's data and store
-// nothing.  The sample's audio range and accumulator offset are loaded at
-// the start, beside the segment table; the rest after the stream (done
-// earlier, the loads cost the stream more than they save): lane l < 16
-// pair l's normalisers (pair = (flagged KV head i, query head g),
-// l = i * G + g), lane 16 + i the bounds of flagged KV head i's segment,
-// every thread its token's logits for all pairs and its accumulator entry,
-// all in one round trip.  The weights exp2(x - max) / sum are summed over
-// each segment's heads, then over the segments, then added to the
-// accumulator entry -- logit_score_kernel's order and validity rules, so
-// the sums are bit-identical to that pass; the entry is stored at the end
-// of the launch.
+// Deferred scoring of the previous launch's kept logits, before this
+// launch's stream.  Workgroup i < the slice count takes slice i = (sample b,
+// block of 256 audio tokens), one token per thread; the other workgroups do
+// nothing of it.  At the start, beside the segment table: the sample's
+// audio range and accumulator offset, lane l < 16 pair l's normalisers
+// (pair = (flagged KV head i, query head g), l = i * G + g), lane 16 + i the
+// bounds of flagged KV head i's segment, every thread its token's logits
+// for all pairs; the accumulator entry once the offset is in.  The weights
+// exp2(x - max) / sum are summed over each segment's heads, then over the
+// segments, then added to the accumulator entry -- logit_score_kernel's
+// order and validity rules, so the sums are bit-identical to that pass --
+// and the entry is stored before the first steps are issued.
 static constexpr int kPrevLogits = 16;  // pairs per sample the deferred form takes (<= 8 KV heads)
 struct PrevLoads {
   float x[kPrevLogits];
@@ -131,15 +129,13 @@ struct PrevLoads {
   int32_t a0, a1, off;  // the sample's audio range and accumulator offset
   float prior;          // the token's accumulator entry
   // the entry's address, and whether it is stored (bit 0), the offset is
-  // valid (bit 1), the workgroup has a slice (bit 2), the slice is its
-  // sample's first (bit 3)
+  // valid (bit 1), the slice is its sample's first (bit 3)
   float* dst;
   int32_t flags;
 };
 
-__device__ __forceinline__ int prev_slice(const AttnParams& p) {
-  return (int32_t)blockIdx.x < p.pv_slices ? (int)blockIdx.x : 0;
-}
+// (called by workgroups with a slice only)
+__device__ __forceinline__ int prev_slice(const AttnParams&) { return (int)blockIdx.x; }
 
 __device__ __forceinline__ void prev_issue_head(const AttnParams& p, PrevLoads& pl) {
   const int b = prev_slice(p) / p.pv_nblk;
@@ -196,9 +192,7 @@ __device__ __forceinline__ void prev_issue_body(const AttnParams& p, int tid, Pr
   const int n_audio = pl.a1 - pl.a0;
   const int64_t j = (int64_t)blk * 256 + tid;
   const bool off_ok = off >= 0 && (int64_t)off + n_audio <= p.pv_acc_len;
-  const bool has_slice = (int32_t)blockIdx.x < p.pv_slices;
-  pl.flags = ((has_slice && off_ok && j < n_audio && j < p.max_audio) ? 1 : 0) | (off_ok ? 2 : 0) |
-             (has_slice ? 4 : 0) | (blk == 0 ? 8 : 0);
+  pl.flags = ((off_ok && j < n_audio && j < p.max_audio) ? 1 : 0) | (off_ok ? 2 : 0) | (blk == 0 ? 8 : 0);
 }
 
 // The token's accumulator entry (at, -1: none) and its new value, from
@@ -207,8 +201,7 @@ __device__ __forceinline__ void prev_finish(const AttnParams& p, int tid, const 
                                             float& total) {
   dst = nullptr;
   total = 0.f;
-  const int flags = __builtin_amdgcn_readfirstlane(pl.flags);  // bits 1, 2, 3 are uniform
-  if (!(flags & 4)) return;  // uniform: slice 0's data, loaded for the wait counts only
+  const int flags = __builtin_amdgcn_readfirstlane(pl.flags);  // bits 1 and 3 are uniform
   if (!(flags & 2)) {  // the accumulator cannot hold the sample's tokens
     if (tid == 0 && (flags & 8)) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
     return;
@@ -1199,12 +1192,22 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   // the walk)
   int32_t t_lo = 0, t_hi = 0, t_cap = 0;
   int64_t t_base = 0;
+  // XL: the scored flag of the segment's KV head and its sample's audio
+  // range, independent of the table: loaded beside it, not behind it
+  int32_t t_xm = 0, t_as = 0, t_ae = 0;
   if constexpr (DIRECT) {
     const int si = min((int)(threadIdx.x & 63), nseg_arg - 1);
     t_lo = cu_arg[si];
     t_hi = cu_arg[si + 1];
     if (base_arg) t_base = base_arg[si];
     if (APPEND) t_cap = cap_arg[si];
+    if (XL) {
+      const int hkv = max(p.Hkv, 1);
+      const int smp = si / hkv;
+      t_xm = p.xmask[si - smp * hkv];
+      t_as = p.audio_s[smp];
+      t_ae = p.audio_e[smp];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   const int64_t grid = (int64_t)((uint32_t)gpack_arg >> 8);
@@ -1223,11 +1226,20 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   p.split_inv = inv_arg;
   p.n_seg = nseg_arg;
   p.G = g_arg;
-  // deferred scoring: the sample's audio range and accumulator offset,
-  // loaded beside the segment table
+  // deferred scoring, before the stream: the sample's audio range and
+  // accumulator offset, the slot's normalisers, the segments' bounds and the
+  // logits go out beside the segment table, the accumulator entry once the
+  // offset is in; the sums and the entry's store come before the first
+  // steps are issued (workgroups with a slice only)
   PrevLoads pl;
   static_assert(!PV || (DIRECT && APPEND), "deferred scoring rides in the direct, fused-append instances");
-  if constexpr (PV) prev_issue_head(p, pl);
+  const bool pv_slice = PV && (int32_t)blockIdx.x < p.pv_slices;  // uniform
+  if constexpr (PV) {
+    if (pv_slice) {
+      prev_issue_head(p, pl);
+      prev_issue_body(p, (int)threadIdx.x, pl);
+    }
+  }
   using G_ = StreamGeom<D>;
   using Ops = StreamOps<T>;
   constexpr int NT = NW * 64;
@@ -1352,9 +1364,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
         llen = hi - lo;
         lneg = llen < 0;
         if (APPEND) lcap = DIRECT ? t_cap : p.cap[s];
-        if (XL && p.xmask[s % p.Hkv]) {
-          la0 = p.audio_s[s / p.Hkv];
-          lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
+        if (XL && (DIRECT ? t_xm : p.xmask[s % p.Hkv])) {
+          la0 = DIRECT ? t_as : p.audio_s[s / p.Hkv];
+          lal = (int32_t)max((int64_t)0, min((int64_t)(DIRECT ? t_ae : p.audio_e[s / p.Hkv]) - la0, p.max_audio));
         }
       }
     }
@@ -1548,12 +1560,20 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       mx = fmaxf(mx, x[i]);
     }
     if (XL && st.alen > 0 && st.t0 < st.alen && st.t0 + st.nrows > 0 && lc < G) {
-      // rows of a scored segment's audio: keep their logits for the scoring pass
+      // rows of a scored segment's audio: keep their logits for the scoring
+      // pass.  The lane's four rows are consecutive in the slot: one 16-byte
+      // store (4-byte aligned) when all four are kept, else one per row.
       WNW_GLOBAL float* xl = gptr_w<float>(p.xlog) + ((int64_t)st.s * G + lc) * p.max_audio;
+      const int r0 = 4 * lq, t0 = st.t0 + r0;
+      if (r0 + 3 < st.nrows && t0 >= 0 && t0 + 3 < st.alen) {
+        typedef float f32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+        *(WNW_GLOBAL f32x4a4*)(xl + t0) = f32x4a4{x[0], x[1], x[2], x[3]};
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * lq + i, t = st.t0 + r;
-        if (r < st.nrows && t >= 0 && t < st.alen) xl[t] = x[i];
+        for (int i = 0; i < 4; ++i) {
+          const int r = r0 + i, t = t0 + i;
+          if (r < st.nrows && t >= 0 && t < st.alen) xl[t] = x[i];
+        }
       }
     }
     mx = max_x32(max_x16(mx));
@@ -1651,6 +1671,14 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     }
   };
 
+  if constexpr (PV) {
+    if (pv_slice) {
+      float* pv_dst = nullptr;
+      float pv_total = 0.f;
+      prev_finish(p, tid, pl, pv_dst, pv_total);
+      if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
+    }
+  }
   // ---- the stream: two steps in flight (buffers 0 and 1 alternate)
   SStep sA, sB;
   bool hA = gen(sA);
@@ -1710,13 +1738,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     if (!hA) break;
   }
   wait_vmcnt<0>();
-  // deferred scoring, after the stream: every load of the stream is in, so
-  // the compiler's wait counts for these loads hold (it does not count the
-  // stream's own loads).  They arrive while the waves' states are merged
-  // and the hand-off runs; the sums and the store come at the kernel's end
-  // (summing right after the partials' wait was slower: 26.5 against
-  // 26.3 us per cfg2 layer-step with scoring).
-  if constexpr (PV) prev_issue_body(p, tid, pl);
 
   // ---- shared pieces: merge the waves' states through LDS
   __syncthreads();  // every wave is done with its step buffers (reused below)
@@ -1912,12 +1933,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       if (lane == p.n_seg - 1) co[p.n_seg] = llo + llen + p.n_seg;  // llen: cu[s + 1] - cu[s], as read
       if (!lneg && llen + 1 > lcap) raise_device_error(p.err, WNW_DEVERR_CAPACITY);
     }
-  }
-  if constexpr (PV) {
-    float* pv_dst = nullptr;
-    float pv_total = 0.f;
-    prev_finish(p, tid, pl, pv_dst, pv_total);
-    if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
   }
 }
 
