@@ -250,6 +250,24 @@ __device__ __forceinline__ void prev_finish(const AttnParams& p, int tid, const 
   }
 }
 
+// side rows (256 bytes: one dword per lane) of the scored flags and audio
+// ranges, per wave (direct table, logits kept)
+static constexpr int kXlRows = 3;
+
+// A 4-byte copy per lane from a 64-bit address into LDS (lane i's dword at
+// lds_addr + 4 i), counted by vmcnt like the stream's loads.
+__device__ __forceinline__ void dma_copy4_a64(const void* gaddr, uint32_t lds_addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(gaddr), "s"(lds_addr)
+      : "memory");
+}
+
 // A segment is attended when its rows fit both row spaces; every piece of
 // logic that decides this (owner outputs, pieces, the stream walk) uses this
 // one test, so all workgroups agree on the segments they skip.
@@ -1146,12 +1164,14 @@ __host__ __device__ constexpr int stream_qslot(int G, int D, bool append) {
 }
 
 // LDS bytes of the streaming kernel: per wave two (K, V) step buffers and two
-// q slots of qslot bytes, and with the fused append the kept new rows
-// (kSaveRows x (K + V rows + 8-byte row index)); the merge slots reuse the
-// step buffers.
-__host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot, bool append = false) {
-  return NW * (4 * kSRows * D * 2 + 2 * qslot + (append ? kSaveRows * (2 * D * 2 + 8) : 0));
+// q slots of qslot bytes, with the fused append the kept new rows
+// (kSaveRows x (K + V rows + 8-byte row index)), and side rows of 256 bytes
+// (the direct table's scored flags and audio ranges, the deferred scoring's
+// loads); the merge slots reuse the step buffers.
+__host__ __device__ constexpr int stream_lds_bytes(int D, int NW, int qslot, bool append = false, int side_rows = 0) {
+  return NW * (4 * kSRows * D * 2 + 2 * qslot + (append ? kSaveRows * (2 * D * 2 + 8) : 0) + side_rows * 256);
 }
+__host__ __device__ constexpr int stream_side_rows(bool xl, bool direct) { return xl && direct ? kXlRows : 0; }
 
 // One step of a wave's stream: rows [row0, row0 + nrows) of segment s.
 struct SStep {
@@ -1192,22 +1212,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   // the walk)
   int32_t t_lo = 0, t_hi = 0, t_cap = 0;
   int64_t t_base = 0;
-  // XL: the scored flag of the segment's KV head and its sample's audio
-  // range, independent of the table: loaded beside it, not behind it
-  int32_t t_xm = 0, t_as = 0, t_ae = 0;
   if constexpr (DIRECT) {
     const int si = min((int)(threadIdx.x & 63), nseg_arg - 1);
     t_lo = cu_arg[si];
     t_hi = cu_arg[si + 1];
     if (base_arg) t_base = base_arg[si];
     if (APPEND) t_cap = cap_arg[si];
-    if (XL) {
-      const int hkv = max(p.Hkv, 1);
-      const int smp = si / hkv;
-      t_xm = p.xmask[si - smp * hkv];
-      t_as = p.audio_s[smp];
-      t_ae = p.audio_e[smp];
-    }
   }
   __builtin_amdgcn_sched_barrier(0);
   const int64_t grid = (int64_t)((uint32_t)gpack_arg >> 8);
@@ -1269,6 +1279,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
   uint8_t* sbuf = dyn + NW * (4 * SB + 2 * qslot) + w * kSaveRows * (2 * RB + 8);
   int64_t* srow = (int64_t*)(sbuf + kSaveRows * 2 * RB);
   int nsaved = 0;
+  // side rows of this wave (direct table, logits kept): the scored flag and
+  // audio range of each segment
+  constexpr int kSide = stream_side_rows(XL, DIRECT);
+  uint8_t* side = dyn + NW * (4 * SB + 2 * qslot + (APPEND ? kSaveRows * (2 * RB + 8) : 0)) + w * kSide * 256;
+  const uint32_t lds_side = __builtin_amdgcn_readfirstlane(lds_address(side));
+  const int32_t* xl_rows = (const int32_t*)side;
   const uint32_t lds_w = __builtin_amdgcn_readfirstlane(lds_address(wbuf));
   const uint32_t lds_q = __builtin_amdgcn_readfirstlane(lds_address(qbuf));
   const T* kp = (const T*)p.k;
@@ -1364,9 +1380,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
         llen = hi - lo;
         lneg = llen < 0;
         if (APPEND) lcap = DIRECT ? t_cap : p.cap[s];
-        if (XL && (DIRECT ? t_xm : p.xmask[s % p.Hkv])) {
-          la0 = DIRECT ? t_as : p.audio_s[s / p.Hkv];
-          lal = (int32_t)max((int64_t)0, min((int64_t)(DIRECT ? t_ae : p.audio_e[s / p.Hkv]) - la0, p.max_audio));
+        if (XL && !DIRECT && p.xmask[s % p.Hkv]) {  // DIRECT: the side rows, read by process()
+          la0 = p.audio_s[s / p.Hkv];
+          lal = (int32_t)max((int64_t)0, min((int64_t)p.audio_e[s / p.Hkv] - la0, p.max_audio));
         }
       }
     }
@@ -1436,8 +1452,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     st.whole = cur_whole;
     st.qslot = piece_no & 1;
     if (XL) {
-      st.t0 = (int32_t)(irow - cur_lo) - cur_a0;
-      st.alen = cur_al;
+      // DIRECT: the offset within the segment (the audio start is subtracted
+      // by process(), from the side rows)
+      st.t0 = (int32_t)(irow - cur_lo) - (DIRECT ? 0 : cur_a0);
+      st.alen = DIRECT ? 0 : cur_al;
     }
     // With more than one window of 64 segments (the table pass), the walk
     // may move on to the next window (next_piece below) before this step is
@@ -1559,20 +1577,26 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       x[i] = (4 * lq + i) < nvalid ? sacc[i] * p.scale_log2 : -INFINITY;
       mx = fmaxf(mx, x[i]);
     }
-    if (XL && st.alen > 0 && st.t0 < st.alen && st.t0 + st.nrows > 0 && lc < G) {
+    int32_t x_t0 = st.t0, x_alen = st.alen;
+    if constexpr (XL && DIRECT) {  // the segment's scored flag and audio range (side rows, landed)
+      const int32_t xm = xl_rows[st.wr], as = xl_rows[64 + st.wr], ae = xl_rows[128 + st.wr];
+      x_alen = xm ? (int32_t)max((int64_t)0, min((int64_t)ae - as, p.max_audio)) : 0;
+      x_t0 = st.t0 - as;
+    }
+    if (XL && x_alen > 0 && x_t0 < x_alen && x_t0 + st.nrows > 0 && lc < G) {
       // rows of a scored segment's audio: keep their logits for the scoring
       // pass.  The lane's four rows are consecutive in the slot: one 16-byte
       // store (4-byte aligned) when all four are kept, else one per row.
       WNW_GLOBAL float* xl = gptr_w<float>(p.xlog) + ((int64_t)st.s * G + lc) * p.max_audio;
-      const int r0 = 4 * lq, t0 = st.t0 + r0;
-      if (r0 + 3 < st.nrows && t0 >= 0 && t0 + 3 < st.alen) {
+      const int r0 = 4 * lq, t0 = x_t0 + r0;
+      if (r0 + 3 < st.nrows && t0 >= 0 && t0 + 3 < x_alen) {
         typedef float f32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
         *(WNW_GLOBAL f32x4a4*)(xl + t0) = f32x4a4{x[0], x[1], x[2], x[3]};
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = r0 + i, t = t0 + i;
-          if (r < st.nrows && t >= 0 && t < st.alen) xl[t] = x[i];
+          if (r < st.nrows && t >= 0 && t < x_alen) xl[t] = x[i];
         }
       }
     }
@@ -1678,6 +1702,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
       prev_finish(p, tid, pl, pv_dst, pv_total);
       if (pv_dst) *gptr_w<float>(pv_dst) = pv_total;
     }
+  }
+  // the scored flag and audio range of each segment (lane = segment) into
+  // the side rows, older than every step's loads, so the first step's waits
+  // cover them (the table path does not wait for them)
+  if constexpr (XL && DIRECT) {
+    const int sx = min(lane, p.n_seg - 1);
+    const int hkv = max(p.Hkv, 1);
+    const int smp = sx / hkv;
+    dma_copy4_a64(p.xmask + (sx - smp * hkv), lds_side);
+    dma_copy4_a64(p.audio_s + smp, lds_side + 256);
+    dma_copy4_a64(p.audio_e + smp, lds_side + 512);
   }
   // ---- the stream: two steps in flight (buffers 0 and 1 alternate)
   SStep sA, sB;
@@ -2159,12 +2194,13 @@ static hipError_t set_lds_limit_once(std::vector<signed char>& done, std::mutex&
 // and device).
 template <typename T, int D, int QD, bool XL, bool APPEND, bool DIRECT, bool PV = false>
 static hipError_t launch_stream_k(const AttnParams& ap, int64_t n_wg, hipStream_t st) {
-  const int lds = stream_lds_bytes(D, kNW, stream_qslot(ap.G, D, APPEND), APPEND);
+  constexpr int side = stream_side_rows(XL, DIRECT);
+  const int lds = stream_lds_bytes(D, kNW, stream_qslot(ap.G, D, APPEND), APPEND, side);
   static std::mutex mu;
   static std::vector<signed char> done;
   const hipError_t attr_err =
       set_lds_limit_once(done, mu, (const void*)&attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT, PV>,
-                         stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND));
+                         stream_lds_bytes(D, kNW, stream_qslot(kMaxGroupS, D, APPEND), APPEND, side));
   if (attr_err != hipSuccess) return attr_err;
   hipLaunchKernelGGL((attn_stream_kernel<T, D, kNW, QD, XL, APPEND, DIRECT, PV>), dim3((unsigned)n_wg), dim3(kNW * 64), lds,
                      st, ap.cu, ap.base, ap.cap, ap.q, ap.k, ap.v, ap.n_seg,
