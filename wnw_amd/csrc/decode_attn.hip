@@ -324,10 +324,11 @@ __device__ __forceinline__ int64_t effective_wgs(int64_t R, int64_t grid = gridD
 }
 // Start of split unit u (of P * kSplitWaves) for R rows: the reciprocal
 // when every workgroup of the grid takes part (R >= gridDim.x), else a
-// division (tiny launches).
+// division (tiny launches; marked unlikely, so it is laid out of the
+// prologue's path).
 __device__ __forceinline__ int64_t split_start(int64_t u, int64_t R, int64_t P, uint64_t inv,
                                               int64_t grid = gridDim.x) {
-  if (P == grid && inv != 0) return unit_start(u, R, inv);
+  if (__builtin_expect(P == grid && inv != 0, 1)) return unit_start(u, R, inv);
   return (u * R) / (P * kSplitWaves);
 }
 // This workgroup's logical row range [B0, B1) for R rows over P workgroups.
