@@ -551,10 +551,12 @@ extern "C" int wnw_compact_segments(const void* src_k, const void* src_v, void* 
   return WNW_OK;
 }
 
-void wnw_touch_append_kernels() {
+namespace wnw {
+void touch_append_kernels() {
   hipFuncAttributes a;
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::compact_segments_kernel);
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::append_inplace_kernel);
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::rebuild_append_kernel<false>);
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::interleave_append_kernel<true>);
+  (void)hipFuncGetAttributes(&a, (const void*)&compact_segments_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&append_inplace_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&rebuild_append_kernel<false>);
+  (void)hipFuncGetAttributes(&a, (const void*)&interleave_append_kernel<true>);
 }
+}  // namespace wnw

@@ -78,19 +78,23 @@ extern "C" int wnw_init(void) {
   return WNW_OK;
 }
 
-// Each source file's kernels of the decode path, resolved on the current
-// device (the runtime sets a kernel up the first time it is used).
-void wnw_touch_score_kernels();
-void wnw_touch_topk_kernels();
-void wnw_touch_transfer_kernels();
-void wnw_touch_append_kernels();
-void wnw_touch_offload_kernels();
+// Each source file's kernels of the default decode path (the scoring pass,
+// the chunk top-k, the stage permute, the slack compaction, in-place and
+// dense appends and rebuild, the host-row gather), resolved on the current
+// device: the runtime sets a kernel up the first time it is used.
+namespace wnw {
+void touch_score_kernels();
+void touch_topk_kernels();
+void touch_transfer_kernels();
+void touch_append_kernels();
+void touch_offload_kernels();
+}  // namespace wnw
 extern "C" int wnw_prepare_kernels(void) {
-  wnw_touch_score_kernels();
-  wnw_touch_topk_kernels();
-  wnw_touch_transfer_kernels();
-  wnw_touch_append_kernels();
-  wnw_touch_offload_kernels();
+  wnw::touch_score_kernels();
+  wnw::touch_topk_kernels();
+  wnw::touch_transfer_kernels();
+  wnw::touch_append_kernels();
+  wnw::touch_offload_kernels();
   return WNW_OK;
 }
 

@@ -114,7 +114,9 @@ extern "C" int wnw_gather_host_rows(const void* host_k, const void* host_v, int6
   return WNW_OK;
 }
 
-void wnw_touch_offload_kernels() {
+namespace wnw {
+void touch_offload_kernels() {
   hipFuncAttributes a;
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::gather_host_rows_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&gather_host_rows_kernel);
 }
+}  // namespace wnw

@@ -771,7 +771,9 @@ extern "C" int wnw_fused_score_accumulate(const void* q, const void* k, const in
 // First-use set-up of this file's kernels on the current device (the runtime
 // resolves a kernel the first time it is used: ~2 ms on MI355X); called by
 // wnw_prepare_kernels.
-void wnw_touch_score_kernels() {
+namespace wnw {
+void touch_score_kernels() {
   hipFuncAttributes a;
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::logit_score_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&logit_score_kernel);
 }
+}  // namespace wnw

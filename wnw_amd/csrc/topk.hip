@@ -242,7 +242,9 @@ extern "C" int wnw_chunk_topk(const float* score_acc, int64_t acc_len, const int
   return WNW_OK;
 }
 
-void wnw_touch_topk_kernels() {
+namespace wnw {
+void touch_topk_kernels() {
   hipFuncAttributes a;
-  (void)hipFuncGetAttributes(&a, (const void*)&wnw::chunk_topk_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&chunk_topk_kernel);
 }
+}  // namespace wnw

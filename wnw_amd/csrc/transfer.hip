@@ -689,7 +689,9 @@ extern "C" int wnw_h2d_join(wnw_h2d* x) {
   return x->error;
 }
 
-void wnw_touch_transfer_kernels() {
+namespace wnw {
+void touch_transfer_kernels() {
   hipFuncAttributes a;
-  (void)hipFuncGetAttributes(&a, (const void*)&stage_permute_kernel);
+  (void)hipFuncGetAttributes(&a, (const void*)&::stage_permute_kernel);
 }
+}  // namespace wnw
