@@ -445,7 +445,7 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
     for (int u = 0; u < 4; ++u) {
       const int i = i0 + u * NT + tid;
       if (i >= N) continue;
-      if (APPEND && pid == 0) {  // post-append offsets
+      if (__builtin_expect(APPEND && pid == 0, 0)) {  // post-append offsets (one workgroup)
         WNW_GLOBAL int32_t* co = gptr_w<int32_t>(p.cu_out);
         co[i] = lo[u] + i;
         if (i == N - 1) co[N] = hi[u] + N;
@@ -453,16 +453,19 @@ __device__ __forceinline__ void schedule(const AttnParams& p, int D, SchedLds& s
       int64_t len = (int64_t)hi[u] - lo[u];
       const int64_t b = p.base ? bs[u] : (int64_t)lo[u];
       bool neg = false;
-      if (len < 0) {  // corrupt offsets: treated as an empty segment
+      if (__builtin_expect(len < 0, 0)) {  // corrupt offsets: treated as an empty segment
         raise_device_error(p.err, WNW_DEVERR_ORDER);
         sl.order_bad = 1;
         len = 0;
         neg = true;
-      } else if (APPEND && len + 1 > cp[u]) {
+      } else if (__builtin_expect(APPEND && len + 1 > cp[u], 0)) {
         raise_device_error(p.err, WNW_DEVERR_CAPACITY);
       }
       const bool owner = (i % (int)gridDim.x) == (int)pid;
-      if (!seg_valid(lo[u], len, b, R, KV)) {
+      // rare paths (error, empty segments) hinted so, to keep them out of
+      // the pass's straight line: the pass runs once per launch, with the
+      // instruction cache cold
+      if (__builtin_expect(!seg_valid(lo[u], len, b, R, KV), 0)) {
         if (len != 0) raise_device_error(p.err, WNW_DEVERR_BOUNDS);
         if (APPEND && len == 0 && !neg) {  // only the new row: it is the output
           if (owner) append_only_segment<T>(p, D, i, b, len + 1 <= cp[u] && b >= 0 && b < KV);
