@@ -291,22 +291,32 @@ def _slack_layer(rng, lens, D, dtype, dev, slack=8):
                 cap=t(cap.astype(np.int32)), rows=rows)
 
 
-def test_deferred_scoring_matches_the_scoring_pass():
-    """wnw_decode_attn_append_deferred over a sequence of layers (scored,
-    scored, not scored, scored, then the last slot scored on its own) gives
-    the same outputs, pools, offsets and accumulator bits as
-    q1_decode_attn_score's append form (attention + its own scoring pass)
-    layer by layer, and the accumulator matches the oracle."""
+# (KV heads, group, samples, the layers' scored-head masks: None = a layer
+# that keeps nothing), within the deferred form's 16 scored (KV head, query
+# head) pairs
+_DEFERRED_CASES = [
+    (4, 4, 4, [[1, 0, 1, 0], [0, 1, 1, 0], None, [1, 1, 0, 1]]),
+    (2, 8, 3, [[1, 1], [0, 1], [1, 0], None, [1, 1]]),
+    (4, 7, 2, [[1, 0, 0, 1], None, [0, 1, 0, 0], [0, 0, 1, 1]]),
+]
+
+
+@pytest.mark.parametrize("H,G,B,masks", _DEFERRED_CASES)
+def test_deferred_scoring_matches_the_scoring_pass(H, G, B, masks):
+    """wnw_decode_attn_append_deferred over a sequence of layers (scored and
+    not scored, then the last slot scored on its own) gives the same
+    outputs, pools, offsets and accumulator bits as q1_decode_attn_score's
+    append form (attention + its own scoring pass) layer by layer, and the
+    accumulator matches the oracle."""
     dev = torch.device("cuda", 0)
-    rng = np.random.default_rng(77)
-    H, G, D, B = 4, 4, 128, 4
+    rng = np.random.default_rng(77 + G)
+    D = 128
     n = B * H
     dtype = "bfloat16"
-    a_s = [3, 0, 5, 1]
-    a_e = [900, 700, 1000, 650]
+    a_s = [3, 0, 5, 1][:B]
+    a_e = [900, 700, 1000, 650][:B]
     max_audio = max(e - s for s, e in zip(a_s, a_e))
     offs = np.concatenate([[0], np.cumsum(np.array(a_e) - np.array(a_s))]).astype(np.int32)
-    masks = [[1, 0, 1, 0], [0, 1, 1, 0], None, [1, 1, 0, 1]]
     t = lambda a, dt=torch.int32: torch.from_numpy(np.asarray(a)).to(dt).to(dev)  # noqa: E731
     layers = []
     for li in range(len(masks)):
