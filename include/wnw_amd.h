@@ -607,6 +607,12 @@ int wnw_planner_get_evictions(wnw_planner* p, int32_t* starts, int32_t* ends,
                               int64_t cap);
 /* The `ranges` [n, 2] tensor of compute_and_prepare's result tuple */
 int wnw_planner_get_ranges(wnw_planner* p, int32_t* ranges, int64_t cap);
+/* The last plan's [L+1] layer pointer into `ranges` (layer l's ranges are
+ * [layer_ptr[l], layer_ptr[l+1]); all zero when nothing changed).  No
+ * counterpart in the reference: the offload channel splits the ranges into
+ * groups of layers with it. */
+int wnw_planner_get_range_layers(wnw_planner* p, int32_t* layer_ptr,
+                                 int64_t cap);
 
 /* Offload channel                                                           */
 /* ------------------------------------------------------------------------ */

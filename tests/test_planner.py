@@ -140,6 +140,21 @@ def compare_plan(plan, flag, total, ev_s, ev_e, ranges, outs, L):
     assert ev_e.tolist() == [x for l in range(L) for x in plan.evict_ends[l]]
 
 
+def check_range_layers(ptr, plan, L):
+    """The native layer pointer into the ranges: from 0 to the number of
+    ranges, non-decreasing, and layer l's ranges hold exactly the rows the
+    oracle loads into layer l (sum of its load_lens)."""
+    assert len(ptr) == L + 1
+    if not plan.any_change:
+        assert ptr == [0] * (L + 1)
+        return
+    assert ptr[0] == 0 and ptr[L] == len(plan.cpu_ranges)
+    for l in range(L):
+        assert ptr[l] <= ptr[l + 1]
+        rows = sum(e - s for s, e in plan.cpu_ranges[ptr[l]:ptr[l + 1]])
+        assert rows == sum(plan.load_lens[l]), f"layer {l}"
+
+
 # ---------------------------------------------------------------------------
 def test_oracle_hand_example():
     """1 layer, 1 sample, KV heads 0 (class A) and 1 (class B), 3 segments."""
@@ -196,6 +211,7 @@ def test_native_matches_oracle_multistep(seed):
         flag, total, ev_s, ev_e, ranges = p.compute_and_prepare(
             torch.tensor(flat, dtype=torch.int32), torch.tensor(off, dtype=torch.int32), **outs)
         compare_plan(plan, flag, total, ev_s, ev_e, ranges, outs, L)
+        check_range_layers(p.range_layers(), plan, L)
         for b in range(sc["B"]):
             assert p.get_loaded_segments(b) == sorted(o.loaded[b])
         if not plan.any_change:

@@ -80,6 +80,7 @@ _SIGNATURES = {
     "wnw_planner_compute_and_prepare": (_i32, [_vp] * 14),
     "wnw_planner_get_evictions": (_i32, [_vp, _vp, _vp, _i64]),
     "wnw_planner_get_ranges": (_i32, [_vp, _vp, _i64]),
+    "wnw_planner_get_range_layers": (_i32, [_vp, _vp, _i64]),
     "wnw_h2d_create": (_vp, [_i32]),
     "wnw_h2d_destroy": (None, [_vp]),
     "wnw_h2d_start": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp]),

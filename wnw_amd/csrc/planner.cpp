@@ -59,6 +59,7 @@ struct wnw_planner {
   // results of the last compute_and_prepare
   std::vector<int32_t> ev_starts, ev_ends;
   std::vector<Range> ranges;
+  std::vector<int32_t> range_layer_ptr;  // [L + 1] first range of each layer
   // host restore rows and pinned staging (caller-owned)
   const char* cpu_k = nullptr;
   const char* cpu_v = nullptr;
@@ -286,6 +287,7 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
   p->ev_starts.clear();
   p->ev_ends.clear();
   p->ranges.clear();
+  p->range_layer_ptr.assign((size_t)L + 1, 0);
   *any_change = change ? 1 : 0;
   *total_rows = 0;
   *n_evict = 0;
@@ -304,6 +306,7 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
     int32_t* ls = load_starts_2d + (size_t)l * N;
     int32_t* ll = load_lens_2d + (size_t)l * N;
     int32_t* eo = evict_offsets_2d + (size_t)l * (N + 1);
+    p->range_layer_ptr[l] = (int32_t)p->ranges.size();
     for (int f = 0; f < N; ++f) {
       nl[f] = lens_l[f] + 1;
       ls[f] = -1;
@@ -376,6 +379,7 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
     }
   }
   evict_layer_ptr[L] = (int32_t)p->ev_starts.size();
+  p->range_layer_ptr[L] = (int32_t)p->ranges.size();
   p->seq_lens = std::move(new_lens);
   p->prev_changed = true;
   *total_rows = transfer;
@@ -407,5 +411,18 @@ extern "C" int wnw_planner_get_ranges(wnw_planner* p, int32_t* ranges, int64_t c
     ranges[2 * i] = p->ranges[i].start;
     ranges[2 * i + 1] = p->ranges[i].end;
   }
+  return WNW_OK;
+}
+
+// The last plan's [L + 1] layer pointer into its host ranges: the ranges of
+// layer l are [layer_ptr[l], layer_ptr[l + 1]) (layer-major transfer order).
+extern "C" int wnw_planner_get_range_layers(wnw_planner* p, int32_t* layer_ptr, int64_t cap) {
+  P_CHECK(p, "planner: null handle");
+  P_CHECK(layer_ptr && cap >= (int64_t)p->L + 1, "planner: layer pointer output holds %lld, need %d",
+          (long long)cap, p->L + 1);
+  if (p->range_layer_ptr.empty())
+    memset(layer_ptr, 0, sizeof(int32_t) * (size_t)(p->L + 1));
+  else
+    memcpy(layer_ptr, p->range_layer_ptr.data(), sizeof(int32_t) * (size_t)(p->L + 1));
   return WNW_OK;
 }

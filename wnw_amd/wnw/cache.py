@@ -1151,11 +1151,11 @@ class WnWCache(FlatVarlenCache):
         if pending is None:
             return torch.empty(0, dtype=torch.int32), torch.zeros(self.batch_size + 1, dtype=torch.int32)
         self._tk_event.synchronize()
-        flat, off = [], [0]
-        for row in pending.tolist():
-            flat += [c for c in row if c >= 0]
-            off.append(len(flat))
-        return torch.tensor(flat, dtype=torch.int32), torch.tensor(off, dtype=torch.int32)
+        a = pending.numpy()
+        keep = a >= 0
+        off = np.zeros(a.shape[0] + 1, dtype=np.int32)
+        np.cumsum(keep.sum(axis=1), out=off[1:])
+        return torch.from_numpy(a[keep].astype(np.int32)), torch.from_numpy(off)
 
     def _compute_decode_chunk_update(self) -> bool:
         """cache.py:578-593 + the chunk changes (:609-649): top-k per sample
@@ -1165,8 +1165,8 @@ class WnWCache(FlatVarlenCache):
         return self._plan(topk, off)
 
     def _plan(self, topk: Tensor, off: Tensor) -> bool:
-        flag, total, ev_s, ev_e, ranges = self._planner.compute_and_prepare(topk, off, **self._plan_out)
-        self._plan_result = (total, ev_s, ev_e, ranges)
+        flag, total, ev_s, ev_e, ranges = self._planner.compute_and_prepare(topk, off, check=False, **self._plan_out)
+        self._plan_result = (total, ev_s, ev_e, ranges, self._planner.range_layers() if total > 0 else None)
         return bool(flag)
 
     def _prepare_decode_rebuild_if_needed(self, any_change: bool, activate: bool = True) -> None:
@@ -1180,7 +1180,7 @@ class WnWCache(FlatVarlenCache):
         """cache.py:756-889 with the native plan: the host rows' transfer
         started first (its gather threads run while the rest is prepared),
         then the per-layer descriptors on the device."""
-        total, ev_s, ev_e, ranges = self._plan_result
+        total, ev_s, ev_e, ranges, range_layers = self._plan_result
         self._clear_pending_rebuild_state()
         o = self._plan_out
         dev = self.device
@@ -1188,7 +1188,7 @@ class WnWCache(FlatVarlenCache):
         if total > 0 and self._offload == "device":
             self._gather_loads_on_device(total, ranges, o["load_lens_2d"])
         elif total > 0:
-            self._copy_loads(total, ranges, o["load_lens_2d"])
+            self._copy_loads(total, ranges, range_layers)
         else:
             self._pending_gpu_k = torch.empty(0, self.head_dim, dtype=dt, device=dev)
             self._pending_gpu_v = torch.empty(0, self.head_dim, dtype=dt, device=dev)
@@ -1254,18 +1254,14 @@ class WnWCache(FlatVarlenCache):
         self._pending_layer_events = events
         self._waited_events = set()  # these events are new (an id could repeat a dropped one's)
 
-    def _layer_groups(self, ranges: Tensor, load_lens_2d: Tensor) -> tuple[list[int], list[int]]:
+    def _layer_groups(self, range_layers: list[int]) -> tuple[list[int], list[int]]:
         """Groups of consecutive layers for a plan's loads: the range index
-        bounds of each group and each layer's group.  Ranges are in transfer
-        order (layer, sample, head, segment), so each layer's ranges are
-        contiguous."""
-        r = ranges.numpy()
-        dst = np.zeros(r.shape[0] + 1, dtype=np.int64)
-        np.cumsum(r[:, 1].astype(np.int64) - r[:, 0], out=dst[1:])
-        ends = np.searchsorted(dst, np.cumsum(load_lens_2d.numpy().astype(np.int64).sum(axis=1))).tolist()
+        bounds of each group and each layer's group, from the planner's layer
+        pointer into its ranges (transfer order (layer, sample, head,
+        segment): each layer's ranges are contiguous)."""
         bounds, group_of = [0], []
         for l0, l1 in self._group_layers():
-            bounds.append(ends[l1 - 1])
+            bounds.append(range_layers[l1])
             group_of += [len(bounds) - 2] * (l1 - l0)
         return bounds, group_of
 
@@ -1280,7 +1276,7 @@ class WnWCache(FlatVarlenCache):
         cuts = [0, first] + [first + (L - first) * g // (n - 1) for g in range(1, n)]
         return [(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
 
-    def _copy_loads(self, total: int, ranges: Tensor, load_lens_2d: Tensor) -> None:
+    def _copy_loads(self, total: int, ranges: Tensor, range_layers: list[int]) -> None:
         """The plan's host ranges to the device through the transfer engine,
         group of layers by group on the transfer stream, a layer's rebuild
         waiting for its own group only: copied by the DMA engines straight
@@ -1289,7 +1285,7 @@ class WnWCache(FlatVarlenCache):
         staging pair that the DMA engines copy ("staged").  Returns without
         waiting."""
         dev = self.device
-        bounds, group_of = self._layer_groups(ranges, load_lens_2d)
+        bounds, group_of = self._layer_groups(range_layers)
         stream = self._get_transfer_stream()
         if self._h2d is None:
             self._h2d = HostToDevice()
@@ -1297,11 +1293,9 @@ class WnWCache(FlatVarlenCache):
         with torch.cuda.stream(stream):  # the copies into them follow on this stream
             if direct:
                 stg_k, stg_v = self._device_stage(total)
-            pk = torch.empty(total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
-            pv = torch.empty(total, self.head_dim, dtype=self.cpu_restore_v.dtype, device=dev)
-        compute = torch.cuda.current_stream(dev)
-        pk.record_stream(compute)
-        pv.record_stream(compute)
+            kv = torch.empty(2, total, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
+        kv.record_stream(torch.cuda.current_stream(dev))
+        pk, pv = kv[0], kv[1]
         if direct:
             self._h2d.start_direct(self.cpu_restore_k, self.cpu_restore_v, ranges, bounds, stg_k, stg_v, pk, pv,
                                    stream, check=False)

@@ -108,17 +108,22 @@ class Planner:
 
     def compute_and_prepare(self, topk_idx, topk_off, load_starts_2d: torch.Tensor, load_lens_2d: torch.Tensor,
                             cu_new_2d: torch.Tensor, new_lens_2d: torch.Tensor, evict_offsets_2d: torch.Tensor,
-                            evict_max: torch.Tensor, evict_layer_ptr: torch.Tensor):
+                            evict_max: torch.Tensor, evict_layer_ptr: torch.Tensor, check: bool = True):
         """Returns ``(any_change, total, ev_s, ev_e, ranges)`` like the
         reference (planner.cpp:124-306): ints, int32 [E], int32 [E],
-        int32 [nr, 2]; the 2-D outputs are written in place."""
+        int32 [nr, 2]; the 2-D outputs are written in place.
+        ``check=False`` skips the Python checks of the output tensors, for a
+        caller that made them once with the right shapes (the library still
+        checks every index it reads)."""
         L, N = self.L, self.N
-        shapes = ((load_starts_2d, (L, N)), (load_lens_2d, (L, N)), (cu_new_2d, (L, N + 1)),
-                  (new_lens_2d, (L, N)), (evict_offsets_2d, (L, N + 1)), (evict_max, (L,)),
-                  (evict_layer_ptr, (L + 1,)))
-        for t, shape in shapes:
-            if t.dtype != torch.int32 or t.device.type != "cpu" or not t.is_contiguous() or tuple(t.shape) != shape:
-                raise _lib.WnwError(f"planner output must be a contiguous CPU int32 tensor of shape {shape}")
+        if check:
+            shapes = ((load_starts_2d, (L, N)), (load_lens_2d, (L, N)), (cu_new_2d, (L, N + 1)),
+                      (new_lens_2d, (L, N)), (evict_offsets_2d, (L, N + 1)), (evict_max, (L,)),
+                      (evict_layer_ptr, (L + 1,)))
+            for t, shape in shapes:
+                if t.dtype != torch.int32 or t.device.type != "cpu" or not t.is_contiguous() or \
+                        tuple(t.shape) != shape:
+                    raise _lib.WnwError(f"planner output must be a contiguous CPU int32 tensor of shape {shape}")
         tk, to = _i32(topk_idx), _i32(topk_off)
         if to.numel() != self.B + 1:
             raise _lib.WnwError("topk_off must have batch + 1 entries")
@@ -134,3 +139,10 @@ class Planner:
         self._check(self._lib.wnw_planner_get_evictions(self._h, _p(ev_s), _p(ev_e), n_ev.value), "get_evictions")
         self._check(self._lib.wnw_planner_get_ranges(self._h, _p(ranges), n_rg.value), "get_ranges")
         return int(flag.value), int(total.value), ev_s, ev_e, ranges
+
+    def range_layers(self) -> list[int]:
+        """The last plan's layer pointer into its ``ranges`` (L + 1 entries;
+        layer l's ranges are rows [ptr[l], ptr[l + 1]) of ``ranges``)."""
+        out = (ctypes.c_int32 * (self.L + 1))()
+        self._check(self._lib.wnw_planner_get_range_layers(self._h, out, self.L + 1), "get_range_layers")
+        return list(out)
