@@ -1928,8 +1928,6 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_stream_kernel(const int32_t* 
     }
   }
   wait_vmem();
-  // deferred scoring: its loads are in (the wait above), so its sums cost
-  // no wait here; the accumulator entry is stored at the end
   __syncthreads();  // partials complete; the slots may be overwritten below
   // Both arrivals in one atomic instruction (lanes 0 and 1 of wave 0, one
   // memory round trip); each segment whose last partial this is merges.
