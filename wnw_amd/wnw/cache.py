@@ -662,7 +662,12 @@ class WnWCache(FlatVarlenCache):
         # "device", a gather kernel reading the pinned restore rows itself
         #   (its reads of host memory outrun the copy engine, but the compute
         #   kernels that run meanwhile slow down by more than that)
-        self._load_groups = 8  # groups (copies + events) per plan: copy/compute overlap vs per-copy cost
+        # groups (copies + events) per plan: copy/compute overlap against
+        # per-copy cost.  Six (at 30 layers a first group of two layers):
+        # one layer's spans are too short for the copy engines (each copy
+        # takes about as long to submit as to move), so a one-layer first
+        # group left the link partly idle at the start of every plan
+        self._load_groups = 6
         mode = os.environ.get("WNW_OFFLOAD", "copy")
         if mode not in ("copy", "staged", "device"):
             raise ValueError(f"WNW_OFFLOAD must be 'copy', 'staged' or 'device', got {mode!r}")
