@@ -663,10 +663,12 @@ class WnWCache(FlatVarlenCache):
         #   (its reads of host memory outrun the copy engine, but the compute
         #   kernels that run meanwhile slow down by more than that)
         # groups (copies + events) per plan: copy/compute overlap against
-        # per-copy cost.  Six (at 30 layers a first group of two layers):
-        # one layer's spans are too short for the copy engines (each copy
-        # takes about as long to submit as to move), so a one-layer first
-        # group left the link partly idle at the start of every plan
+        # per-copy cost.  Six: at 30 layers groups of 3, 6, 6, 6, 6 and 3
+        # layers.  One layer's spans are too short for the copy engines
+        # (each copy takes about as long to submit as to move), so a
+        # one-layer first group left the link partly idle at the start of
+        # every plan; the short last group shortens what runs after the
+        # plan's last copy
         self._load_groups = 6
         mode = os.environ.get("WNW_OFFLOAD", "copy")
         if mode not in ("copy", "staged", "device"):
@@ -1271,14 +1273,19 @@ class WnWCache(FlatVarlenCache):
         return bounds, group_of
 
     def _group_layers(self) -> list[tuple[int, int]]:
-        """Layer spans of the load groups: a short first group (the first
-        layer's rows arrive after a small gather and copy), the other layers
-        split evenly over the remaining groups."""
+        """Layer spans of the load groups: a short first group (its rows
+        arrive early), a short last group (its layers are what runs after
+        the plan's last copy) and the other layers split evenly over the
+        groups between; the short groups hold a tenth of the layers (at
+        least one)."""
         L, n = self.num_layers, max(1, min(self._load_groups, self.num_layers))
         if n == 1:
             return [(0, L)]
-        first = max(1, L // (2 * n))
-        cuts = [0, first] + [first + (L - first) * g // (n - 1) for g in range(1, n)]
+        edge = max(1, L // 10)
+        if n == 2:
+            return [(0, edge), (edge, L)]
+        lo, hi, m = edge, L - edge, n - 2
+        cuts = [0] + [lo + (hi - lo) * g // m for g in range(m + 1)] + [L]
         return [(a, b) for a, b in zip(cuts[:-1], cuts[1:]) if b > a]
 
     def _copy_loads(self, total: int, ranges: Tensor, range_layers: list[int]) -> None:
