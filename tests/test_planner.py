@@ -345,3 +345,16 @@ def test_native_rejects_bad_indices():
         p.set_loaded(0, torch.tensor([sc["seg_count"][0] + 5], dtype=torch.int32))
     with pytest.raises(_lib.WnwError):
         p.set_class_b(0, torch.tensor([sc["H"]], dtype=torch.int32))
+
+
+def test_range_layers_before_any_plan_and_short_output():
+    """Before any plan the layer pointer is all zeros; an output shorter than
+    L + 1 entries is refused (no write past it)."""
+    import ctypes
+
+    from wnw_amd import _lib
+    sc = make_scenario(11)
+    p = make_native(sc, 2)
+    assert p.range_layers() == [0] * (sc["L"] + 1)
+    short = (ctypes.c_int32 * sc["L"])()
+    assert _lib.lib().wnw_planner_get_range_layers(p._h, short, sc["L"]) != 0
