@@ -613,6 +613,33 @@ int wnw_planner_get_ranges(wnw_planner* p, int32_t* ranges, int64_t cap);
  * groups of layers with it. */
 int wnw_planner_get_range_layers(wnw_planner* p, int32_t* layer_ptr,
                                  int64_t cap);
+/*
+ * The offload channel's plan step in one call: no counterpart in the
+ * reference, which plans (planner.cpp:124-306, compute_and_prepare) and then
+ * starts its side-stream copy (wnw/code/cache.py:868-881) from Python.
+ * topk: [batch, k] chosen chunks per sample, -1 = none (chunk_topk's
+ * output); the planner's outputs and *any_change, *total_rows, *n_evict,
+ * *n_ranges as for wnw_planner_compute_and_prepare.  Then, when the plan
+ * loads rows and they fit stage_rows and dev_rows, it starts
+ * wnw_h2d_start_direct of its ranges on engine x, in n_groups groups of
+ * consecutive layers (group g: layers [layer_cuts[g], layer_cuts[g+1]),
+ * layer_cuts[n_groups] = the planner's layer count), and sets *started to
+ * 1; otherwise *started is 0 and the caller starts the transfer itself
+ * (the plan stands either way).  The evict lists and ranges are read with
+ * wnw_planner_get_evictions / wnw_planner_get_ranges as after
+ * compute_and_prepare.  It saves the caller's round trips between the
+ * planner and the engine on the step's critical path.
+ */
+int wnw_h2d_plan_start_direct(
+    wnw_h2d* x, wnw_planner* p, const int32_t* topk, int64_t batch, int64_t k,
+    int32_t* load_starts_2d, int32_t* load_lens_2d, int32_t* cu_new_2d,
+    int32_t* new_lens_2d, int32_t* evict_offsets_2d, int32_t* evict_max,
+    int32_t* evict_layer_ptr, const int32_t* layer_cuts, int n_groups,
+    const void* host_k, const void* host_v, int64_t host_rows, void* stage_k,
+    void* stage_v, int64_t stage_rows, void* dev_k, void* dev_v,
+    int64_t dev_rows, int64_t row_bytes, void* stream, int32_t* any_change,
+    int64_t* total_rows, int64_t* n_evict, int64_t* n_ranges,
+    int32_t* started);
 
 /* Offload channel                                                           */
 /* ------------------------------------------------------------------------ */

@@ -44,6 +44,14 @@ def recording(cls):
                 o = off.tolist()
                 self.rec_topk.append([topk.tolist()[o[b]:o[b + 1]] for b in range(self.batch_size)])
             return super()._plan(topk, off)
+
+        def _plan_and_start(self, pending):
+            # the fused plan step reads the pinned [B, k] choice (-1: none)
+            # itself; the planner takes each row's chosen chunks in order
+            if not torch.cuda.is_current_stream_capturing():
+                self._tk_event.synchronize()
+                self.rec_topk.append([[c for c in row if c >= 0] for row in pending.tolist()])
+            return super()._plan_and_start(pending)
     return Rec
 
 

@@ -86,6 +86,9 @@ _SIGNATURES = {
     "wnw_h2d_start": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp]),
     "wnw_h2d_start_direct": (_i32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _i64,
                                     _vp]),
+    "wnw_h2d_plan_start_direct": (_i32, [_vp, _vp, _vp, _i64, _i64] + [_vp] * 8 + [_i32, _vp, _vp, _i64, _vp, _vp,
+                                                                            _i64, _vp, _vp, _i64, _i64, _vp]
+                                  + [_vp] * 5),
     "wnw_h2d_wait": (_i32, [_vp, _i32, _vp]),
     "wnw_h2d_join": (_i32, [_vp]),
     "wnw_h2d_reserve": (_i32, [_vp, _i64, _i32, _vp]),

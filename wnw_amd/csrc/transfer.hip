@@ -509,6 +509,28 @@ int make_job(Job& j, const void* host_k, const void* host_v, int64_t host_rows, 
   return WNW_OK;
 }
 
+// Direct form: the stage rows of each range -- each group's rows [dst[a],
+// dst[b]) hold its ranges in host order, so that ranges touching in host
+// memory are one span.
+void set_stage_rows(Job& j, int n_groups) {
+  const int64_t n_ranges = (int64_t)j.ranges.size() / 2;
+  j.direct = true;
+  j.stage_of.assign(n_ranges, 0);
+  std::vector<int64_t> ord;
+  for (int g = 0; g < n_groups; ++g) {
+    const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
+    ord.resize(b - a);
+    for (int64_t r = a; r < b; ++r) ord[r - a] = r;
+    std::stable_sort(ord.begin(), ord.end(),
+                     [&](int64_t u, int64_t v) { return j.ranges[2 * u] < j.ranges[2 * v]; });
+    int64_t at = j.dst[a];
+    for (int64_t r : ord) {
+      j.stage_of[r] = at;
+      at += (int64_t)j.ranges[2 * r + 1] - j.ranges[2 * r];
+    }
+  }
+}
+
 // Hands a job to the lead thread (after the previous job is fully issued).
 void submit(wnw_h2d* x, Job&& j, int n_groups) {
   {
@@ -554,23 +576,62 @@ extern "C" int wnw_h2d_start_direct(wnw_h2d* x, const void* host_k, const void* 
   WNW_CHECK_ARG(n_ranges == 0 || (((uintptr_t)stage_k | (uintptr_t)stage_v | (uintptr_t)dev_k | (uintptr_t)dev_v) &
                                   15) == 0,
                 "h2d: stage and device rows must be 16-byte aligned");
-  // stage rows: each group's rows [dst[a], dst[b]) hold its ranges in host order
-  j.direct = true;
-  j.stage_of.assign(n_ranges, 0);
-  std::vector<int64_t> ord;
-  for (int g = 0; g < n_groups; ++g) {
-    const int64_t a = j.group_ranges[g], b = j.group_ranges[g + 1];
-    ord.resize(b - a);
-    for (int64_t r = a; r < b; ++r) ord[r - a] = r;
-    std::stable_sort(ord.begin(), ord.end(),
-                     [&](int64_t u, int64_t v) { return j.ranges[2 * u] < j.ranges[2 * v]; });
-    int64_t at = j.dst[a];
-    for (int64_t r : ord) {
-      j.stage_of[r] = at;
-      at += (int64_t)j.ranges[2 * r + 1] - j.ranges[2 * r];
-    }
-  }
+  set_stage_rows(j, n_groups);
   submit(x, std::move(j), n_groups);
+  return WNW_OK;
+}
+
+extern "C" int wnw_h2d_plan_start_direct(wnw_h2d* x, wnw_planner* p, const int32_t* topk, int64_t batch, int64_t k,
+                                         int32_t* load_starts_2d, int32_t* load_lens_2d, int32_t* cu_new_2d,
+                                         int32_t* new_lens_2d, int32_t* evict_offsets_2d, int32_t* evict_max,
+                                         int32_t* evict_layer_ptr, const int32_t* layer_cuts, int n_groups,
+                                         const void* host_k, const void* host_v, int64_t host_rows, void* stage_k,
+                                         void* stage_v, int64_t stage_rows, void* dev_k, void* dev_v,
+                                         int64_t dev_rows, int64_t row_bytes, void* stream, int32_t* any_change,
+                                         int64_t* total_rows, int64_t* n_evict, int64_t* n_ranges,
+                                         int32_t* started) {
+  WNW_CHECK_ARG(x && p && started && layer_cuts, "h2d: null argument");
+  WNW_CHECK_ARG(batch >= 0 && k >= 0 && (batch * k == 0 || topk), "h2d: bad top-k choice");
+  WNW_CHECK_ARG(n_groups >= 1 && n_groups <= kMaxGroups && layer_cuts[0] == 0,
+                "h2d: n_groups must be in [1, %d] with layer cuts from 0", kMaxGroups);
+  WNW_CHECK_ARG(row_bytes > 0 && row_bytes % 16 == 0, "h2d: row_bytes must be a positive multiple of 16");
+  *started = 0;
+  // the choice as the planner's CSR (-1: no chunk)
+  std::vector<int32_t> flat, off(batch + 1, 0);
+  flat.reserve((size_t)(batch * k));
+  for (int64_t b = 0; b < batch; ++b) {
+    for (int64_t c = 0; c < k; ++c)
+      if (topk[b * k + c] >= 0) flat.push_back(topk[b * k + c]);
+    off[b + 1] = (int32_t)flat.size();
+  }
+  const int rc = wnw_planner_compute_and_prepare(p, flat.data(), off.data(), load_starts_2d, load_lens_2d, cu_new_2d,
+                                                 new_lens_2d, evict_offsets_2d, evict_max, evict_layer_ptr,
+                                                 any_change, total_rows, n_evict, n_ranges);
+  if (rc != WNW_OK) return rc;
+  // nothing to load, or more rows than the caller's buffers: the caller
+  // takes it from here
+  if (!*any_change || *total_rows == 0 || *total_rows > stage_rows || *total_rows > dev_rows) return WNW_OK;
+  const int L = layer_cuts[n_groups];
+  for (int g = 0; g < n_groups; ++g)
+    WNW_CHECK_ARG(layer_cuts[g] <= layer_cuts[g + 1], "h2d: layer cuts decrease");
+  std::vector<int32_t> lp(L + 1);
+  int rc2 = wnw_planner_get_range_layers(p, lp.data(), L + 1);
+  if (rc2 != WNW_OK) return rc2;
+  WNW_CHECK_ARG(lp[L] == *n_ranges, "h2d: the layer cuts end at layer %d, not the planner's last", L);
+  std::vector<int64_t> gr(n_groups + 1);
+  for (int g = 0; g <= n_groups; ++g) gr[g] = lp[layer_cuts[g]];
+  std::vector<int32_t> rg((size_t)(2 * *n_ranges));
+  rc2 = wnw_planner_get_ranges(p, rg.data(), *n_ranges);
+  if (rc2 != WNW_OK) return rc2;
+  Job j;
+  rc2 = make_job(j, host_k, host_v, host_rows, rg.data(), *n_ranges, gr.data(), n_groups, stage_k, stage_v,
+                 stage_rows, dev_k, dev_v, dev_rows, row_bytes, stream);
+  if (rc2 != WNW_OK) return rc2;
+  WNW_CHECK_ARG((((uintptr_t)stage_k | (uintptr_t)stage_v | (uintptr_t)dev_k | (uintptr_t)dev_v) & 15) == 0,
+                "h2d: stage and device rows must be 16-byte aligned");
+  set_stage_rows(j, n_groups);
+  submit(x, std::move(j), n_groups);
+  *started = 1;
   return WNW_OK;
 }
 

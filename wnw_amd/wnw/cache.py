@@ -679,6 +679,7 @@ class WnWCache(FlatVarlenCache):
         self._offload = mode
         self._h2d = None
         self._stage = None
+        self._started_loads = None  # (K rows, V rows, group of each layer) of a transfer started with its plan
         self._staging_rows_hint = self._plan_rows_bound()
         dt = self.cpu_restore_k.dtype
         if mode == "staged" and self._staging_rows_hint > 0:
@@ -1166,10 +1167,43 @@ class WnWCache(FlatVarlenCache):
 
     def _compute_decode_chunk_update(self) -> bool:
         """cache.py:578-593 + the chunk changes (:609-649): top-k per sample
-        from this step's scores, then the native plan of every layer."""
+        from this step's scores, then the native plan of every layer (with
+        the direct transfer, the plan and the start of its loads in one
+        native call)."""
         self._pending_chunk_update = False
-        topk, off = self._topk_finalize(self._topk_scores_async())
+        pending = self._topk_scores_async()
+        if pending is not None and self._offload == "copy" and self._staging_rows_hint > 0:
+            return self._plan_and_start(pending)
+        topk, off = self._topk_finalize(pending)
         return self._plan(topk, off)
+
+    def _plan_and_start(self, pending: Tensor) -> bool:
+        """``_topk_finalize`` + ``_plan`` + the start of ``_copy_loads``'s
+        direct transfer, with the planner and the transfer engine in one
+        native call (``wnw_h2d_plan_start_direct``): the time from the top-k
+        to the first copy is on every offload step's critical path.  The
+        loaded rows' buffers are taken at the plan bound before the wait,
+        while the device still runs the step's last layers."""
+        dev = self.device
+        stream = self._get_transfer_stream()
+        if self._h2d is None:
+            self._h2d = HostToDevice()
+        bound = self._staging_rows_hint
+        with torch.cuda.stream(stream):  # the copies into them follow on this stream
+            stg_k, stg_v = self._device_stage(bound)
+            kv = torch.empty(2, bound, self.head_dim, dtype=self.cpu_restore_k.dtype, device=dev)
+        kv.record_stream(torch.cuda.current_stream(dev))
+        cuts = [a for a, _ in self._group_layers()] + [self.num_layers]
+        self._tk_event.synchronize()
+        flag, total, n_ev, n_rg, started = self._h2d.plan_start_direct(
+            self._planner, pending, self._plan_out, cuts, self.cpu_restore_k, self.cpu_restore_v, stg_k, stg_v,
+            kv[0], kv[1], stream)
+        ev_s, ev_e, ranges = self._planner.plan_lists(n_ev, n_rg)
+        range_layers = self._planner.range_layers() if total > 0 else None
+        self._plan_result = (total, ev_s, ev_e, ranges, range_layers)
+        if started:
+            self._started_loads = (kv[0, :total], kv[1, :total], self._layer_groups(range_layers)[1])
+        return bool(flag)
 
     def _plan(self, topk: Tensor, off: Tensor) -> bool:
         flag, total, ev_s, ev_e, ranges = self._planner.compute_and_prepare(topk, off, check=False, **self._plan_out)
@@ -1188,12 +1222,16 @@ class WnWCache(FlatVarlenCache):
         started first (its gather threads run while the rest is prepared),
         then the per-layer descriptors on the device."""
         total, ev_s, ev_e, ranges, range_layers = self._plan_result
+        started, self._started_loads = self._started_loads, None
         self._clear_pending_rebuild_state()
         o = self._plan_out
         dev = self.device
         dt = self.layer_k[0].dtype
         if total > 0 and self._offload == "device":
             self._gather_loads_on_device(total, ranges, o["load_lens_2d"])
+        elif total > 0 and started is not None:  # started with the plan (_plan_and_start)
+            self._pending_gpu_k, self._pending_gpu_v, group_of = started
+            self._pending_layer_events = [("h2d", g) for g in group_of]
         elif total > 0:
             self._copy_loads(total, ranges, range_layers)
         else:

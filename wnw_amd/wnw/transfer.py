@@ -102,6 +102,35 @@ class HostToDevice:
             len(group_ranges) - 1, _lib.ptr(stage_k), _lib.ptr(stage_v), stage_k.shape[0], _lib.ptr(dev_k),
             _lib.ptr(dev_v), dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream)), "h2d start_direct")
 
+    def plan_start_direct(self, planner, topk: torch.Tensor, outs: dict, layer_cuts: list[int],
+                          host_k: torch.Tensor, host_v: torch.Tensor, stage_k: torch.Tensor, stage_v: torch.Tensor,
+                          dev_k: torch.Tensor, dev_v: torch.Tensor, stream: torch.cuda.Stream):
+        """``wnw_h2d_plan_start_direct``: the planner's compute_and_prepare
+        from the device top-k's choice (``topk``, a CPU int32 [B, k] tensor,
+        -1 = none; ``outs`` its output tensors, as for compute_and_prepare),
+        then, if the plan loads rows that fit the stage and device rows, the
+        direct transfer of its ranges in the groups of layers ``layer_cuts``
+        describes.  Returns ``(any_change, total, n_evict, n_ranges,
+        started)``; with ``started`` False the caller starts the transfer
+        itself.  The tensors are the caller's, right by construction (the
+        library checks every index and size)."""
+        tk = topk.contiguous()
+        cuts = (ctypes.c_int32 * len(layer_cuts))(*layer_cuts)
+        flag, started = ctypes.c_int32(0), ctypes.c_int32(0)
+        total, n_ev, n_rg = ctypes.c_int64(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        o = outs
+        row_bytes = host_k.shape[1] * host_k.element_size()
+        _lib.check(_lib.lib().wnw_h2d_plan_start_direct(
+            self._h, planner._h, _lib.ptr(tk), tk.shape[0], tk.shape[1] if tk.dim() == 2 else 0,
+            _lib.ptr(o["load_starts_2d"]), _lib.ptr(o["load_lens_2d"]), _lib.ptr(o["cu_new_2d"]),
+            _lib.ptr(o["new_lens_2d"]), _lib.ptr(o["evict_offsets_2d"]), _lib.ptr(o["evict_max"]),
+            _lib.ptr(o["evict_layer_ptr"]), cuts, len(layer_cuts) - 1, _lib.ptr(host_k), _lib.ptr(host_v),
+            host_k.shape[0], _lib.ptr(stage_k), _lib.ptr(stage_v), stage_k.shape[0], _lib.ptr(dev_k),
+            _lib.ptr(dev_v), dev_k.shape[0], row_bytes, ctypes.c_void_p(stream.cuda_stream), ctypes.byref(flag),
+            ctypes.byref(total), ctypes.byref(n_ev), ctypes.byref(n_rg), ctypes.byref(started)),
+            "h2d plan_start_direct")
+        return int(flag.value), int(total.value), int(n_ev.value), int(n_rg.value), bool(started.value)
+
     def reserve(self, n_ranges: int, stream: torch.cuda.Stream, groups: int = 8) -> None:
         """Pays the engine's set-up costs now (``wnw_h2d_reserve``): the
         direct form's copy streams on the current device, descriptor room for

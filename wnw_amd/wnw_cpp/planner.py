@@ -133,12 +133,19 @@ class Planner:
             self._h, _p(tk), _p(to), _p(load_starts_2d), _p(load_lens_2d), _p(cu_new_2d), _p(new_lens_2d),
             _p(evict_offsets_2d), _p(evict_max), _p(evict_layer_ptr), ctypes.byref(flag), ctypes.byref(total),
             ctypes.byref(n_ev), ctypes.byref(n_rg)), "compute_and_prepare")
-        ev_s = torch.empty(n_ev.value, dtype=torch.int32)
-        ev_e = torch.empty(n_ev.value, dtype=torch.int32)
-        ranges = torch.empty(n_rg.value, 2, dtype=torch.int32)
-        self._check(self._lib.wnw_planner_get_evictions(self._h, _p(ev_s), _p(ev_e), n_ev.value), "get_evictions")
-        self._check(self._lib.wnw_planner_get_ranges(self._h, _p(ranges), n_rg.value), "get_ranges")
+        ev_s, ev_e, ranges = self.plan_lists(n_ev.value, n_rg.value)
         return int(flag.value), int(total.value), ev_s, ev_e, ranges
+
+    def plan_lists(self, n_evict: int, n_ranges: int):
+        """The last plan's evict lists and host ranges (``ev_s``, ``ev_e``,
+        ``ranges`` of compute_and_prepare's result), ``n_evict`` and
+        ``n_ranges`` long."""
+        ev_s = torch.empty(n_evict, dtype=torch.int32)
+        ev_e = torch.empty(n_evict, dtype=torch.int32)
+        ranges = torch.empty(n_ranges, 2, dtype=torch.int32)
+        self._check(self._lib.wnw_planner_get_evictions(self._h, _p(ev_s), _p(ev_e), n_evict), "get_evictions")
+        self._check(self._lib.wnw_planner_get_ranges(self._h, _p(ranges), n_ranges), "get_ranges")
+        return ev_s, ev_e, ranges
 
     def range_layers(self) -> list[int]:
         """The last plan's layer pointer into its ``ranges`` (L + 1 entries;
