@@ -297,6 +297,12 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
     return WNW_OK;
   }
 
+  // the sets as sorted vectors for the layer loop (same order)
+  std::vector<std::vector<int32_t>> tl(B), te(B);
+  for (int b = 0; b < B; ++b) {
+    tl[b].assign(to_load[b].begin(), to_load[b].end());
+    te[b].assign(to_evict[b].begin(), to_evict[b].end());
+  }
   std::vector<int32_t> new_lens((size_t)L * N);
   int32_t transfer = 0;
   std::vector<std::pair<int32_t, int32_t>> ev;
@@ -315,14 +321,14 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
     // the evict ranges of flat segment f are emitted in f order below
     std::vector<std::vector<std::pair<int32_t, int32_t>>> ev_f(N);
     for (int b = 0; b < B; ++b) {
-      if (to_load[b].empty() && to_evict[b].empty()) continue;
+      if (tl[b].empty() && te[b].empty()) continue;
       const int sc = p->seg_count[b];
       for (int h : p->class_b[l]) {
         const int f = b * H + h;
         SegMeta* m = p->metas(l, f);
         int32_t evicted = 0;
         ev.clear();
-        for (int32_t s : to_evict[b]) {
+        for (int32_t s : te[b]) {
           if (m[s].cpu_s >= 0 && m[s].gpu_s >= 0) {
             ev.emplace_back(m[s].gpu_s, m[s].gpu_e);
             m[s].gpu_s = m[s].gpu_e = -1;
@@ -331,8 +337,10 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
         std::sort(ev.begin(), ev.end());
         for (auto& r : ev) evicted += r.second - r.first;
         if (!ev.empty()) {
+          // (an evicted segment's gpu rows were cleared just above, so the
+          // resident test alone leaves it out)
           for (int s = 0; s < sc; ++s) {
-            if (m[s].cpu_s < 0 || m[s].gpu_s < 0 || to_evict[b].count(s)) continue;
+            if (m[s].cpu_s < 0 || m[s].gpu_s < 0) continue;
             int32_t shift = 0;
             for (auto& r : ev)
               if (r.second <= m[s].gpu_s) shift += r.second - r.first;
@@ -343,7 +351,7 @@ extern "C" int wnw_planner_compute_and_prepare(wnw_planner* p, const int32_t* to
         ev_f[f] = ev;
         int32_t cursor = lens_l[f] - evicted;
         int32_t loaded_rows = 0;
-        for (int32_t s : to_load[b]) {  // std::set: ascending segment order
+        for (int32_t s : tl[b]) {  // ascending segment order
           if (m[s].cpu_s < 0) continue;
           const int32_t n = m[s].cpu_e - m[s].cpu_s;
           p->ranges.push_back({m[s].cpu_s, m[s].cpu_e});
