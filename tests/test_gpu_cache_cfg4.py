@@ -51,9 +51,21 @@ def _config():
                      prefill_score_mode="last", num_layers=L, num_kv_heads=HKV, num_q_heads=HQ)
 
 
-@pytest.mark.parametrize("fused,offload", [(True, "copy"), (False, "copy"), (True, "staged"), (True, "device")])
-def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
+@pytest.mark.parametrize("fused,offload,small", [(True, "copy", False), (False, "copy", False), (True, "staged", False),
+                                                 (True, "device", False), (True, "copy", True)])
+def test_cfg4_decode_steps_match_simulation(fused, offload, small, monkeypatch):
+    """``small``: the copy path's plan step (the planner and the transfer's
+    start in one native call) is given loaded-row buffers too small for the
+    plans, so it leaves every transfer to the Python start (``_copy_loads``);
+    otherwise the copy path never falls back to it."""
     dev = torch.device("cuda", 0)
+    n_py_starts = [0]
+    py_start = WnWCache._copy_loads
+
+    def counted(self, *a, **k):
+        n_py_starts[0] += 1
+        return py_start(self, *a, **k)
+    monkeypatch.setattr(WnWCache, "_copy_loads", counted)
     # the transfer engine (DMA copies straight from the host rows, or host
     # gather threads + DMA copies, per group of layers) or the device gather
     # kernel reading pinned memory
@@ -66,7 +78,8 @@ def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
     cache.setup_audio(torch.tensor([TEXT], device=dev), torch.tensor([TEXT + AUDIO], device=dev), None)
     gen = torch.Generator(device=dev)
     gen.manual_seed(11)
-    print(f"cfg4 cache test fused={fused} offload={offload}: prefill of {L} layers x {S} tokens", flush=True)
+    print(f"cfg4 cache test fused={fused} offload={offload} small={small}: prefill of {L} layers x {S} tokens",
+          flush=True)
     for layer in range(L):
         k = torch.randn(B, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16)
         v = torch.randn(B, HKV, S, D, device=dev, generator=gen).to(torch.bfloat16)
@@ -78,6 +91,8 @@ def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
     torch.cuda.synchronize()
     assert _lib.device_error() == 0
     assert cache._offload == offload
+    if small:
+        cache._staging_rows_hint = 16  # the plan step's buffers (the stage made at set-up stays)
     assert cache.cpu_restore_k.shape[0] > 6 * L * (AUDIO - AUDIO // CHUNK * KEEP) // 2  # most class-B audio on host
     sim = DecodeSimulation(cache, [(TEXT, TEXT + AUDIO)])
     scale = D ** -0.5
@@ -95,3 +110,6 @@ def test_cfg4_decode_steps_match_simulation(fused, offload, monkeypatch):
     assert sim.n_plans >= STEPS - 2, "random scores change the chunk choice nearly every step"
     assert sim.n_loaded_rows > 0
     assert cache.layout_counts["relocate"] > 0, cache.layout_counts
+    if offload == "copy":
+        # with room, every transfer starts with its plan; without, none does
+        assert (n_py_starts[0] > 0) == small, n_py_starts[0]
