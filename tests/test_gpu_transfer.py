@@ -215,3 +215,29 @@ def test_arguments_are_checked():
     eng.join()
     torch.cuda.synchronize()
     eng.close()
+
+
+def test_plan_start_direct_checks_the_planner_geometry():
+    """The fused plan step refuses a choice for another batch size, or layer
+    cuts that do not end at the planner's layer count, before planning."""
+    from wnw_amd.wnw_cpp.planner import Planner
+    dev = torch.device("cuda", 0)
+    L, H, B = 3, 4, 2
+    planner = Planner(L, H, B, 2)
+    x = HostToDevice(workers=1)
+    hk = torch.zeros(64, 64, dtype=torch.bfloat16, pin_memory=True)
+    hv = torch.zeros_like(hk).pin_memory()
+    st = [torch.zeros(64, 64, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    N = B * H
+    outs = dict(load_starts_2d=torch.empty(L, N, dtype=torch.int32), load_lens_2d=torch.empty(L, N, dtype=torch.int32),
+                cu_new_2d=torch.empty(L, N + 1, dtype=torch.int32), new_lens_2d=torch.empty(L, N, dtype=torch.int32),
+                evict_offsets_2d=torch.empty(L, N + 1, dtype=torch.int32), evict_max=torch.empty(L, dtype=torch.int32),
+                evict_layer_ptr=torch.empty(L + 1, dtype=torch.int32))
+    stream = torch.cuda.current_stream(dev)
+    with pytest.raises(_lib.WnwError, match="samples"):
+        x.plan_start_direct(planner, torch.full((B + 1, 2), -1, dtype=torch.int32), outs, [0, 1, L], hk, hv,
+                            st[0], st[1], st[2], st[3], stream)
+    with pytest.raises(_lib.WnwError, match="samples"):
+        x.plan_start_direct(planner, torch.full((B, 2), -1, dtype=torch.int32), outs, [0, 1, L + 1], hk, hv,
+                            st[0], st[1], st[2], st[3], stream)
+    x.close()

@@ -29,6 +29,7 @@
 
 namespace wnw {
 void set_error(const char* fmt, ...);
+void planner_dims(const wnw_planner* p, int* layers, int* batch);
 }
 
 namespace {
@@ -433,4 +434,11 @@ extern "C" int wnw_planner_get_range_layers(wnw_planner* p, int32_t* layer_ptr, 
   else
     memcpy(layer_ptr, p->range_layer_ptr.data(), sizeof(int32_t) * (size_t)(p->L + 1));
   return WNW_OK;
+}
+
+// The planner's layer count and batch size, for the library's own callers
+// (the transfer engine's plan step checks its arguments against them).
+void wnw::planner_dims(const wnw_planner* p, int* layers, int* batch) {
+  *layers = p ? p->L : 0;
+  *batch = p ? p->B : 0;
 }

@@ -595,6 +595,11 @@ extern "C" int wnw_h2d_plan_start_direct(wnw_h2d* x, wnw_planner* p, const int32
   WNW_CHECK_ARG(n_groups >= 1 && n_groups <= kMaxGroups && layer_cuts[0] == 0,
                 "h2d: n_groups must be in [1, %d] with layer cuts from 0", kMaxGroups);
   WNW_CHECK_ARG(row_bytes > 0 && row_bytes % 16 == 0, "h2d: row_bytes must be a positive multiple of 16");
+  int pl_layers = 0, pl_batch = 0;
+  wnw::planner_dims(p, &pl_layers, &pl_batch);
+  WNW_CHECK_ARG(batch == pl_batch && layer_cuts[n_groups] == pl_layers,
+                "h2d: the choice covers %lld samples and the cuts %d layers; the planner has %d and %d",
+                (long long)batch, layer_cuts[n_groups], pl_batch, pl_layers);
   *started = 0;
   // the choice as the planner's CSR (-1: no chunk)
   std::vector<int32_t> flat, off(batch + 1, 0);

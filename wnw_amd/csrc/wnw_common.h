@@ -19,6 +19,8 @@ int32_t* device_error_word();
 // Compute units of the current device (queried once per device; 256 when
 // the query fails).
 int device_cus();
+// The host planner's layer count and batch size (planner.cpp).
+void planner_dims(const wnw_planner* p, int* layers, int* batch);
 
 // Logits of the scored (class-A) audio rows, kept by the streaming attention
 // kernel for the scoring pass: xlog[(s * G + g) * max_audio + t].
