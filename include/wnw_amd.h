@@ -618,7 +618,9 @@ int wnw_planner_get_range_layers(wnw_planner* p, int32_t* layer_ptr,
  * reference, which plans (planner.cpp:124-306, compute_and_prepare) and then
  * starts its side-stream copy (wnw/code/cache.py:868-881) from Python.
  * topk: [batch, k] chosen chunks per sample, -1 = none (chunk_topk's
- * output); the planner's outputs and *any_change, *total_rows, *n_evict,
+ * output; batch = the planner's batch size, and layer_cuts[n_groups] its
+ * layer count, else WNW_EINVAL before planning); the planner's outputs
+ * and *any_change, *total_rows, *n_evict,
  * *n_ranges as for wnw_planner_compute_and_prepare.  Then, when the plan
  * loads rows and they fit stage_rows and dev_rows, it starts
  * wnw_h2d_start_direct of its ranges on engine x, in n_groups groups of
